@@ -1,0 +1,40 @@
+// Internal (non-ABI) launch helpers shared between the translation units.
+#pragma once
+
+#include "dsk_common.hpp"
+
+namespace dsk {
+
+// Grouped GEMM problem: C[m, :] = A[row(m), :] @ B_g^T for m in group g's rows.
+struct GemmArgs {
+  const uint16_t* A;
+  int64_t lda;
+  const int32_t* a_rows;   // optional: A row of output row m is a_rows[m]
+  int a_rows_limit;        // valid A rows are [0, a_rows_limit)
+  const uint16_t* B;
+  int64_t ldb;
+  int64_t b_group_stride;  // elements between consecutive groups' weights
+  uint16_t* C;
+  int64_t ldc;
+  const int32_t* offsets;  // [G+1] group row boundaries, or NULL: one group [0, M)
+  int G;
+  int M, N, K;             // N = output columns (SwiGLU: intermediate size)
+  int up_row_offset;       // SwiGLU: first up row inside a group's weight
+};
+
+int run_gemm(const GemmArgs& a, bool swiglu, hipStream_t st);
+
+int launch_route(const float* logits, int64_t ld, int T, int E, int K, int32_t* idx, float* w,
+                 int32_t* blk_hist, int32_t* local_rank, int32_t* counts, int32_t* offsets,
+                 int32_t* token_map, int32_t* slot_of, int n_extra_groups, hipStream_t st);
+int launch_scan(const int32_t* hist, int nblk, int E, int32_t* counts, int32_t* offsets,
+                int32_t* blk_base, int n_extra_groups, int extra_rows, hipStream_t st);
+int launch_permute(const int32_t* idx, const float* w, int T, int K, int E,
+                   const int32_t* offsets, const int32_t* blk_base, const int32_t* local_rank,
+                   int S, int32_t* token_map, float* dw, int32_t* slot_of, int n_extra_groups,
+                   hipStream_t st);
+int launch_combine_slots(const uint16_t* y, int64_t ldy, const int32_t* slot_of,
+                         const float* topk_w, int T, int K, int H, int extra_base,
+                         int n_extra_groups, uint16_t* out, int64_t ldo, hipStream_t st);
+
+}  // namespace dsk

@@ -1,0 +1,287 @@
+// Bandwidth-bound MLA helper kernels for gfx950: RMSNorm and interleaved RoPE.
+//
+// RMSNorm (reference module src/reference/mla.py:53-64, kernel
+// src/kernels/mla/rms_norm.cu:47-120): y = w * x * rsqrt(mean(x^2) + eps) with
+// fp32 math and one rounding of the output. One wave per row; the row stays in
+// registers between the sum-of-squares pass and the scaling pass, so every
+// element is read from HBM once. Row strides let a strided view (the 512-wide
+// latent inside the 576-wide kv_a output) be normalised without a copy.
+//
+// RoPE (mla.py:176-206, rope.cu:61-95): input pairs (2k, 2k+1) map to outputs
+// k and k + d/2. The pre-indexed cos/sin tables [B, 1, S, d] are broadcast
+// over heads by index arithmetic instead of being materialised per head.
+#include "dsk_common.hpp"
+
+#include <algorithm>
+
+namespace dsk {
+
+template <typename T>
+struct Vec8;
+template <>
+struct Vec8<uint16_t> {
+  static __device__ __forceinline__ void load(const uint16_t* p, float (&x)[8]) {
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(p);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      x[2 * j] = bf16lo(v[j]);
+      x[2 * j + 1] = bf16hi(v[j]);
+    }
+  }
+  static __device__ __forceinline__ void store(uint16_t* p, const float (&x)[8]) {
+    u32x4_t v;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = pack_bf16x2(x[2 * j], x[2 * j + 1]);
+    *reinterpret_cast<u32x4_t*>(p) = v;
+  }
+};
+template <>
+struct Vec8<float> {
+  static __device__ __forceinline__ void load(const float* p, float (&x)[8]) {
+    const floatx4_t a = *reinterpret_cast<const floatx4_t*>(p);
+    const floatx4_t b = *reinterpret_cast<const floatx4_t*>(p + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      x[j] = a[j];
+      x[4 + j] = b[j];
+    }
+  }
+  static __device__ __forceinline__ void store(float* p, const float (&x)[8]) {
+    floatx4_t a, b;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      a[j] = x[j];
+      b[j] = x[4 + j];
+    }
+    *reinterpret_cast<floatx4_t*>(p) = a;
+    *reinterpret_cast<floatx4_t*>(p + 4) = b;
+  }
+};
+
+__device__ __forceinline__ float to_f(uint16_t v) { return bf16_to_f32(v); }
+__device__ __forceinline__ float to_f(float v) { return v; }
+__device__ __forceinline__ void from_f(float v, uint16_t* p) { *p = f32_to_bf16(v); }
+__device__ __forceinline__ void from_f(float v, float* p) { *p = v; }
+
+constexpr int kNormThreads = 256;  // 4 rows per workgroup
+
+// NV = 8-element chunks held per lane in registers (H <= 512 * NV, H % 8 == 0).
+template <typename Tin, typename Tout, int NV>
+__global__ __launch_bounds__(kNormThreads) void rms_norm_vec_kernel(
+    const Tin* __restrict__ in, int64_t ld_in, const float* __restrict__ w,
+    Tout* __restrict__ out, int64_t ld_out, int rows, int H, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * (kNormThreads / 64) + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const Tin* src = in + row * ld_in;
+  float x[NV][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = lane + 64 * j;
+    if (c * 8 < H) {
+      Vec8<Tin>::load(src + c * 8, x[j]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(x[j][e], x[j][e], ss);
+    }
+  }
+  ss = wave_sum(ss);
+  const float r = rsqrtf(ss / (float)H + eps);
+  Tout* dst = out + row * ld_out;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = lane + 64 * j;
+    if (c * 8 < H) {
+      const floatx4_t w0 = *reinterpret_cast<const floatx4_t*>(w + c * 8);
+      const floatx4_t w1 = *reinterpret_cast<const floatx4_t*>(w + c * 8 + 4);
+      float y[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        y[e] = (x[j][e] * r) * w0[e];
+        y[4 + e] = (x[j][4 + e] * r) * w1[e];
+      }
+      Vec8<Tout>::store(dst + c * 8, y);
+    }
+  }
+}
+
+// Any even H: scalar two-pass variant (the row is re-read, typically from L2).
+template <typename Tin, typename Tout>
+__global__ __launch_bounds__(kNormThreads) void rms_norm_scalar_kernel(
+    const Tin* __restrict__ in, int64_t ld_in, const float* __restrict__ w,
+    Tout* __restrict__ out, int64_t ld_out, int rows, int H, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * (kNormThreads / 64) + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const Tin* src = in + row * ld_in;
+  float ss = 0.f;
+  for (int c = lane; c < H; c += 64) {
+    const float v = to_f(src[c]);
+    ss = fmaf(v, v, ss);
+  }
+  ss = wave_sum(ss);
+  const float r = rsqrtf(ss / (float)H + eps);
+  Tout* dst = out + row * ld_out;
+  for (int c = lane; c < H; c += 64) from_f((to_f(src[c]) * r) * w[c], dst + c);
+}
+
+template <typename Tin, typename Tout>
+static int launch_rms_norm(const Tin* in, int64_t ld_in, const float* w, Tout* out,
+                           int64_t ld_out, int rows, int H, float eps, hipStream_t st) {
+  const unsigned grid = (unsigned)(((int64_t)rows + 3) / 4);
+  const bool vec = H % 8 == 0 && H <= 4096 && aligned16(in) && aligned16(out) &&
+                   aligned16(w) && (ld_in * (int64_t)sizeof(Tin)) % 16 == 0 &&
+                   (ld_out * (int64_t)sizeof(Tout)) % 16 == 0;
+  if (vec) {
+    const int nv = (H + 511) / 512;
+    if (nv <= 1)
+      hipLaunchKernelGGL((rms_norm_vec_kernel<Tin, Tout, 1>), dim3(grid), dim3(kNormThreads), 0,
+                         st, in, ld_in, w, out, ld_out, rows, H, eps);
+    else if (nv <= 2)
+      hipLaunchKernelGGL((rms_norm_vec_kernel<Tin, Tout, 2>), dim3(grid), dim3(kNormThreads), 0,
+                         st, in, ld_in, w, out, ld_out, rows, H, eps);
+    else if (nv <= 4)
+      hipLaunchKernelGGL((rms_norm_vec_kernel<Tin, Tout, 4>), dim3(grid), dim3(kNormThreads), 0,
+                         st, in, ld_in, w, out, ld_out, rows, H, eps);
+    else
+      hipLaunchKernelGGL((rms_norm_vec_kernel<Tin, Tout, 8>), dim3(grid), dim3(kNormThreads), 0,
+                         st, in, ld_in, w, out, ld_out, rows, H, eps);
+  } else {
+    hipLaunchKernelGGL((rms_norm_scalar_kernel<Tin, Tout>), dim3(grid), dim3(kNormThreads), 0,
+                       st, in, ld_in, w, out, ld_out, rows, H, eps);
+  }
+  return check_launch("rms_norm_kernel");
+}
+
+// ------------------------------------------------------------------- rope ---
+// One thread per 8 input elements (4 pairs): 16-byte load of x, 8-byte loads of
+// cos/sin at k and k + d/2, two 8-byte stores.
+struct RopeTensor {
+  const uint16_t* x;
+  int64_t sb, sh, ss;
+  uint16_t* out;
+  int heads;
+};
+
+__global__ __launch_bounds__(256) void rope_kernel(RopeTensor a, RopeTensor b, int64_t rows_a,
+                                                   int64_t rows_b,
+                                                   const uint16_t* __restrict__ cos_t,
+                                                   const uint16_t* __restrict__ sin_t,
+                                                   int64_t cb, int64_t cs, int S, int d) {
+  const int cpr = d / 8;
+  const int half = d / 2;
+  const int64_t total = (rows_a + rows_b) * cpr;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    int64_t row = i / cpr;
+    const int c = (int)(i - row * cpr);
+    const RopeTensor& r = row < rows_a ? a : b;
+    if (row >= rows_a) row -= rows_a;
+    const int s = (int)(row % S);
+    const int64_t bh = row / S;
+    const int h = (int)(bh % r.heads);
+    const int bb = (int)(bh / r.heads);
+    const uint16_t* xp = r.x + bb * r.sb + h * r.sh + (int64_t)s * r.ss + c * 8;
+    const int64_t toff = bb * cb + (int64_t)s * cs;
+    const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(xp);
+    const u32x2_t clo = *reinterpret_cast<const u32x2_t*>(cos_t + toff + 4 * c);
+    const u32x2_t chi = *reinterpret_cast<const u32x2_t*>(cos_t + toff + half + 4 * c);
+    const u32x2_t slo = *reinterpret_cast<const u32x2_t*>(sin_t + toff + 4 * c);
+    const u32x2_t shi = *reinterpret_cast<const u32x2_t*>(sin_t + toff + half + 4 * c);
+    float lo[4], hi[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float x0 = bf16lo(xv[j]);  // x[2k]
+      const float x1 = bf16hi(xv[j]);  // x[2k+1]
+      const uint32_t cl = clo[j >> 1], ch = chi[j >> 1], sl = slo[j >> 1], sh = shi[j >> 1];
+      const float c_lo = (j & 1) ? bf16hi(cl) : bf16lo(cl);
+      const float c_hi = (j & 1) ? bf16hi(ch) : bf16lo(ch);
+      const float s_lo = (j & 1) ? bf16hi(sl) : bf16lo(sl);
+      const float s_hi = (j & 1) ? bf16hi(sh) : bf16lo(sh);
+      lo[j] = x0 * c_lo - x1 * s_lo;
+      hi[j] = x1 * c_hi + x0 * s_hi;
+    }
+    uint16_t* op = r.out + row * d;
+    u32x2_t olo, ohi;
+    olo[0] = pack_bf16x2(lo[0], lo[1]);
+    olo[1] = pack_bf16x2(lo[2], lo[3]);
+    ohi[0] = pack_bf16x2(hi[0], hi[1]);
+    ohi[1] = pack_bf16x2(hi[2], hi[3]);
+    *reinterpret_cast<u32x2_t*>(op + 4 * c) = olo;
+    *reinterpret_cast<u32x2_t*>(op + half + 4 * c) = ohi;
+  }
+}
+
+static int check_rope(const void* x, int64_t sb, int64_t sh, int64_t ss, const void* out,
+                      int d) {
+  if (!x || !out) return fail(DSK_ERR_NULL_PTR, "rope: NULL pointer");
+  if (!aligned16(x) || !aligned16(out) || sb % 8 || sh % 8 || ss % 8)
+    return fail(DSK_ERR_ALIGNMENT, "rope: rows must be 16-byte aligned");
+  (void)d;
+  return DSK_OK;
+}
+
+}  // namespace dsk
+
+using namespace dsk;
+
+extern "C" int dsk_rms_norm(const dsk_bf16* in, int64_t ld_in, const float* weight,
+                            dsk_bf16* out, int64_t ld_out, int rows, int hidden, float eps,
+                            void* stream) {
+  DSK_REQUIRE(hidden > 0 && hidden % 2 == 0, DSK_ERR_INVALID_ARG,
+              "rms_norm: hidden_size must be even for bfloat162 vectorisation.");
+  DSK_REQUIRE(rows >= 0, DSK_ERR_INVALID_ARG, "rms_norm: rows < 0");
+  if (rows == 0) return DSK_OK;
+  DSK_REQUIRE(in && weight && out, DSK_ERR_NULL_PTR, "rms_norm: NULL pointer");
+  DSK_REQUIRE(ld_in >= hidden && ld_out >= hidden, DSK_ERR_INVALID_ARG,
+              "rms_norm: row stride < hidden_size");
+  return launch_rms_norm<uint16_t, uint16_t>(in, ld_in, weight, out, ld_out, rows, hidden, eps,
+                                             as_stream(stream));
+}
+
+extern "C" int dsk_rms_norm_f32(const float* in, int64_t ld_in, const float* weight,
+                                float* out, int64_t ld_out, int rows, int hidden, float eps,
+                                void* stream) {
+  DSK_REQUIRE(hidden > 0, DSK_ERR_INVALID_ARG, "rms_norm_f32: hidden_size must be positive");
+  DSK_REQUIRE(rows >= 0, DSK_ERR_INVALID_ARG, "rms_norm_f32: rows < 0");
+  if (rows == 0) return DSK_OK;
+  DSK_REQUIRE(in && weight && out, DSK_ERR_NULL_PTR, "rms_norm_f32: NULL pointer");
+  DSK_REQUIRE(ld_in >= hidden && ld_out >= hidden, DSK_ERR_INVALID_ARG,
+              "rms_norm_f32: row stride < hidden_size");
+  return launch_rms_norm<float, float>(in, ld_in, weight, out, ld_out, rows, hidden, eps,
+                                       as_stream(stream));
+}
+
+extern "C" int dsk_rope_qk(const dsk_bf16* q, int64_t qsb, int64_t qsh, int64_t qss,
+                           const dsk_bf16* k, int64_t ksb, int64_t ksh, int64_t kss,
+                           const dsk_bf16* cos_t, const dsk_bf16* sin_t, int64_t cb,
+                           int64_t cs, dsk_bf16* q_out, dsk_bf16* k_out, int B, int Hq,
+                           int Hk, int S, int d, void* stream) {
+  DSK_REQUIRE(d > 0 && d % 8 == 0 && d <= 256, DSK_ERR_INVALID_ARG,
+              "rope: rope_dim must be a multiple of 8 in [8, 256]");
+  DSK_REQUIRE(B >= 0 && Hq >= 0 && Hk >= 0 && S >= 0, DSK_ERR_INVALID_ARG,
+              "rope: negative size");
+  const int64_t rows_q = (int64_t)B * Hq * S;
+  const int64_t rows_k = (int64_t)B * Hk * S;
+  if (rows_q + rows_k == 0) return DSK_OK;
+  DSK_REQUIRE(cos_t && sin_t, DSK_ERR_NULL_PTR, "rope: cos/sin is NULL");
+  DSK_REQUIRE(aligned16(cos_t) && aligned16(sin_t) && cb % 8 == 0 && cs % 8 == 0,
+              DSK_ERR_ALIGNMENT, "rope: cos/sin rows must be 16-byte aligned");
+  int rc;
+  if (rows_q && (rc = check_rope(q, qsb, qsh, qss, q_out, d))) return rc;
+  if (rows_k && (rc = check_rope(k, ksb, ksh, kss, k_out, d))) return rc;
+  RopeTensor a{q, qsb, qsh, qss, q_out, Hq > 0 ? Hq : 1};
+  RopeTensor b{k, ksb, ksh, kss, k_out, Hk > 0 ? Hk : 1};
+  const int64_t work = (rows_q + rows_k) * (d / 8);
+  const unsigned grid = (unsigned)std::min<int64_t>((work + 255) / 256, 16384);
+  hipLaunchKernelGGL(rope_kernel, dim3(grid), dim3(256), 0, as_stream(stream), a, b, rows_q,
+                     rows_k, cos_t, sin_t, cb, cs, S, d);
+  return check_launch("rope_kernel");
+}
+
+extern "C" int dsk_rope(const dsk_bf16* x, int64_t sb, int64_t sh, int64_t ss,
+                        const dsk_bf16* cos_t, const dsk_bf16* sin_t, int64_t cb, int64_t cs,
+                        dsk_bf16* out, int B, int Hh, int S, int d, void* stream) {
+  return dsk_rope_qk(x, sb, sh, ss, nullptr, 0, 0, 0, cos_t, sin_t, cb, cs, out, nullptr, B, Hh,
+                     0, S, d, stream);
+}

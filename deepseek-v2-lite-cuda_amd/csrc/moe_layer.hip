@@ -1,0 +1,160 @@
+// Fused DeepSeekMoE forward on one GPU: the whole layer (moe.py:77-109) as one
+// C call that enqueues 4-6 kernels on the caller's stream and never waits.
+//
+//   route (+histogram, ranks)  ->  [scan + permute when T > 64]  ->
+//   grouped GEMM1 + SwiGLU (A rows gathered from x through token_map)  ->
+//   grouped GEMM2  ->  combine (ascending-expert fp32 sum + shared rows, one
+//   bf16 rounding)
+//
+// The shared expert (intermediate 2*I) is run as n_shared_groups extra groups
+// of width I appended after the routed experts: group E+j holds gate/up rows
+// [j*I, (j+1)*I) of the shared gate/up weights and the matching column slice of
+// the shared down weight. Every token routes to each of them with weight 1.0,
+// so the shared expert costs no extra launch and rides the same tile scheduler.
+// Slot layout: [0, T*K) routed (expert-major, ascending token), then group E+j
+// rows [T*K + j*T, T*K + (j+1)*T) in token order.
+#include "dsk_internal.hpp"
+
+namespace dsk {
+
+struct FusedLayout {
+  size_t hist, base, rank, idx, w, counts, offsets, token_map, slot_of, h, y, total;
+};
+
+static FusedLayout fused_layout(int T, int E, int K, int nsh, int H, int I) {
+  FusedLayout L{};
+  const int nblk = (T + 63) / 64;
+  const size_t S = (size_t)T * K;
+  const size_t Stot = S + (size_t)nsh * T;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off += align_up(bytes > 0 ? bytes : 1, 256);
+    return o;
+  };
+  L.hist = take((size_t)nblk * E * 4);
+  L.base = take((size_t)nblk * E * 4);
+  L.rank = take(S * 4);
+  L.idx = take(S * 4);
+  L.w = take(S * 4);
+  L.counts = take((size_t)E * 4);
+  L.offsets = take((size_t)(E + nsh + 1) * 4);
+  L.token_map = take(Stot * 4);
+  L.slot_of = take(S * 4);
+  L.h = take(Stot * I * 2);
+  L.y = take(Stot * H * 2);
+  L.total = off;
+  return L;
+}
+
+}  // namespace dsk
+
+using namespace dsk;
+
+extern "C" size_t dsk_moe_fused_workspace_size(int num_tokens, int num_experts, int top_k,
+                                               int n_shared_groups, int hidden,
+                                               int intermediate) {
+  if (num_tokens < 0 || num_experts <= 0 || top_k <= 0 || n_shared_groups < 0) return 0;
+  return fused_layout(num_tokens, num_experts, top_k, n_shared_groups, hidden, intermediate)
+      .total;
+}
+
+extern "C" int dsk_moe_fused_forward(const float* logits, const dsk_bf16* x, const dsk_bf16* w1,
+                                     const dsk_bf16* w2, dsk_bf16* out, int num_tokens,
+                                     int num_experts, int top_k, int n_shared_groups,
+                                     int hidden, int intermediate, int32_t* topk_idx_out,
+                                     float* topk_w_out, int32_t* expert_offsets_out,
+                                     void* workspace, size_t workspace_bytes,
+                                     void* const* stage_events, void* stream) {
+  const int T = num_tokens, E = num_experts, K = top_k, nsh = n_shared_groups;
+  const int H = hidden, I = intermediate;
+  DSK_REQUIRE(E >= 1 && E <= DSK_MAX_EXPERTS, DSK_ERR_INVALID_ARG,
+              "moe_fused: num_experts must be in [1, 64]");
+  DSK_REQUIRE(K >= 1 && K <= DSK_MAX_TOP_K && K <= E, DSK_ERR_INVALID_ARG,
+              "moe_fused: top_k must be in [1, min(6, num_experts)]");
+  DSK_REQUIRE(nsh >= 0 && E + nsh <= 128, DSK_ERR_INVALID_ARG,
+              "moe_fused: too many shared groups");
+  DSK_REQUIRE(T >= 0, DSK_ERR_INVALID_ARG, "moe_fused: num_tokens < 0");
+  DSK_REQUIRE(H > 0 && H % 64 == 0 && I > 0 && I % 64 == 0, DSK_ERR_INVALID_ARG,
+              "moe_fused: hidden and intermediate sizes must be multiples of 64");
+  if (T == 0) return DSK_OK;
+  DSK_REQUIRE(logits && x && w1 && w2 && out, DSK_ERR_NULL_PTR, "moe_fused: NULL pointer");
+  DSK_REQUIRE(aligned16(x) && aligned16(w1) && aligned16(w2) && aligned16(out),
+              DSK_ERR_ALIGNMENT, "moe_fused: tensors must be 16-byte aligned");
+  const FusedLayout L = fused_layout(T, E, K, nsh, H, I);
+  DSK_REQUIRE(workspace != nullptr && workspace_bytes >= L.total && aligned16(workspace),
+              DSK_ERR_WORKSPACE, "moe_fused: workspace too small");
+  hipStream_t st = as_stream(stream);
+  char* ws = static_cast<char*>(workspace);
+  int32_t* hist = reinterpret_cast<int32_t*>(ws + L.hist);
+  int32_t* base = reinterpret_cast<int32_t*>(ws + L.base);
+  int32_t* rank = reinterpret_cast<int32_t*>(ws + L.rank);
+  int32_t* idx = topk_idx_out ? topk_idx_out : reinterpret_cast<int32_t*>(ws + L.idx);
+  float* w = topk_w_out ? topk_w_out : reinterpret_cast<float*>(ws + L.w);
+  int32_t* counts = reinterpret_cast<int32_t*>(ws + L.counts);
+  int32_t* offsets = reinterpret_cast<int32_t*>(ws + L.offsets);
+  int32_t* token_map = reinterpret_cast<int32_t*>(ws + L.token_map);
+  int32_t* slot_of = reinterpret_cast<int32_t*>(ws + L.slot_of);
+  uint16_t* h = reinterpret_cast<uint16_t*>(ws + L.h);
+  uint16_t* y = reinterpret_cast<uint16_t*>(ws + L.y);
+  const int nblk = (T + 63) / 64;
+  const int S = T * K;
+  const int Stot = S + nsh * T;
+  const int G = E + nsh;
+
+  // optional instrumentation: hipEvent_t recorded at the 5 stage boundaries
+  auto mark = [&](int i) -> int {
+    if (stage_events == nullptr || stage_events[i] == nullptr) return DSK_OK;
+    if (hipEventRecord(reinterpret_cast<hipEvent_t>(stage_events[i]), st) != hipSuccess)
+      return fail(DSK_ERR_LAUNCH, "moe_fused: hipEventRecord failed");
+    return DSK_OK;
+  };
+  int rc;
+  if ((rc = mark(0))) return rc;
+  if (nblk == 1) {
+    rc = launch_route(logits, E, T, E, K, idx, w, hist, rank, counts, offsets, token_map,
+                      slot_of, nsh, st);
+    if (rc) return rc;
+  } else {
+    rc = launch_route(logits, E, T, E, K, idx, w, hist, rank, nullptr, nullptr, nullptr,
+                      nullptr, 0, st);
+    if (rc) return rc;
+    rc = launch_scan(hist, nblk, E, counts, offsets, base, nsh, T, st);
+    if (rc) return rc;
+    rc = launch_permute(idx, w, T, K, E, offsets, base, rank, S, token_map, nullptr, slot_of,
+                        nsh, st);
+    if (rc) return rc;
+  }
+
+  if ((rc = mark(1))) return rc;
+
+  GemmArgs g1{};
+  g1.A = x; g1.lda = H;
+  g1.a_rows = token_map; g1.a_rows_limit = T;
+  g1.B = w1; g1.ldb = H; g1.b_group_stride = (int64_t)2 * I * H;
+  g1.C = h; g1.ldc = I;
+  g1.offsets = offsets; g1.G = G;
+  g1.M = Stot; g1.N = I; g1.K = H;
+  g1.up_row_offset = I;
+  if ((rc = run_gemm(g1, true, st))) return rc;
+  if ((rc = mark(2))) return rc;
+
+  GemmArgs g2{};
+  g2.A = h; g2.lda = I;
+  g2.B = w2; g2.ldb = I; g2.b_group_stride = (int64_t)H * I;
+  g2.C = y; g2.ldc = H;
+  g2.offsets = offsets; g2.G = G;
+  g2.M = Stot; g2.N = H; g2.K = I;
+  if ((rc = run_gemm(g2, false, st))) return rc;
+  if ((rc = mark(3))) return rc;
+
+  rc = launch_combine_slots(y, H, slot_of, w, T, K, H, S, nsh, out, H, st);
+  if (rc) return rc;
+  if ((rc = mark(4))) return rc;
+  if (expert_offsets_out != nullptr) {
+    if (hipMemcpyAsync(expert_offsets_out, offsets, (size_t)(E + 1) * 4,
+                       hipMemcpyDeviceToDevice, st) != hipSuccess)
+      return fail(DSK_ERR_LAUNCH, "moe_fused: offsets copy failed");
+  }
+  return DSK_OK;
+}

@@ -1,0 +1,147 @@
+"""Fused MoE forward on MI355X (reference host orchestrator:
+src/kernels/moe_fused.py:89-272).
+
+Two levels are offered, as in the reference:
+  * the op-by-op pipeline `route_dispatch_combine` — the reference's seven-op
+    call sequence (moe_fused.py:118-154) built from this package's ops, plus the
+    shared expert the reference omits;
+  * the fused entry `moe_fused_forward_logits` / `FusedMoELayer` /
+    `fused_moe_forward` — one C call (dsk_moe_fused_forward) that enqueues
+    route -> permutation -> GEMM1+SwiGLU -> GEMM2 -> combine with the shared
+    expert folded into the grouped GEMMs, and no host synchronisation.
+
+The gate logits stay a torch fp32 linear, as at moe_fused.py:131.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import ops
+from ._lib import check, lib, stream_handle
+from .expert_prepack import prepack_experts, prepack_with_shared
+
+
+def moe_fused_forward_logits(logits: torch.Tensor, hidden_states: torch.Tensor,
+                             w1: torch.Tensor, w2: torch.Tensor, top_k: int,
+                             n_shared_groups: int, num_experts: Optional[int] = None,
+                             return_routing: bool = False, stage_events=None,
+                             workspace: Optional[torch.Tensor] = None):
+    """Whole MoE layer from precomputed fp32 gate logits [T, E].
+
+    w1: [E + n_shared_groups, 2I, H] bf16, w2: [E + n_shared_groups, H, I] bf16.
+    Returns out [T, H] bf16 (and (topk_idx, topk_w, expert_offsets) if asked).
+    stage_events: optional ctypes array of 5 hipEvent_t handles recorded at the
+    stage boundaries (instrumentation for benchmarks). workspace: optional
+    preallocated uint8 CUDA buffer of at least dsk_moe_fused_workspace_size bytes."""
+    op = "moe_fused_forward"
+    T, H = hidden_states.shape
+    E = logits.shape[1] if num_experts is None else num_experts
+    G, N2, Hw = w1.shape
+    I = N2 // 2
+    for t, n, dt in ((logits, "logits", torch.float32), (hidden_states, "hidden_states", torch.bfloat16),
+                     (w1, "w1", torch.bfloat16), (w2, "w2", torch.bfloat16)):
+        if not (t.is_cuda and t.is_contiguous() and t.dtype == dt):
+            raise RuntimeError(f"{op}: {n} must be a contiguous CUDA {dt} tensor")
+    if logits.shape != (T, E) or G != E + n_shared_groups or Hw != H or tuple(w2.shape) != (G, H, I):
+        raise RuntimeError(f"{op}: inconsistent shapes logits={tuple(logits.shape)} "
+                           f"x={tuple(hidden_states.shape)} w1={tuple(w1.shape)} w2={tuple(w2.shape)}")
+    dev = hidden_states.device
+    out = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+    if T == 0:
+        return out
+    nws = lib.dsk_moe_fused_workspace_size(T, E, top_k, n_shared_groups, H, I)
+    ws = workspace if workspace is not None and workspace.numel() >= nws else \
+        torch.empty(nws, dtype=torch.uint8, device=dev)
+    if stage_events is not None and not isinstance(stage_events, int):
+        stage_events = ctypes.cast(stage_events, ctypes.c_void_p).value
+    idx = w = offs = None
+    if return_routing:
+        idx = torch.empty((T, top_k), dtype=torch.int32, device=dev)
+        w = torch.empty((T, top_k), dtype=torch.float32, device=dev)
+        offs = torch.empty((E + 1,), dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        check(lib.dsk_moe_fused_forward(
+            logits.data_ptr(), hidden_states.data_ptr(), w1.data_ptr(), w2.data_ptr(),
+            out.data_ptr(), T, E, top_k, n_shared_groups, H, I,
+            idx.data_ptr() if idx is not None else None,
+            w.data_ptr() if w is not None else None,
+            offs.data_ptr() if offs is not None else None,
+            ws.data_ptr(), ws.numel(), stage_events, stream_handle(dev)), op)
+    if return_routing:
+        return out, (idx, w, offs)
+    return out
+
+
+def route_dispatch_combine(hidden_states: torch.Tensor, gate_weight: torch.Tensor,
+                           packed_w1: torch.Tensor, w2: torch.Tensor, top_k: int,
+                           fuse_swiglu: bool = False) -> torch.Tensor:
+    """The reference op sequence (moe_fused.py:118-154) over this package's ops:
+    routing -> scan -> dispatch -> gemm1 -> swiglu -> gemm2 -> combine."""
+    T = hidden_states.shape[0]
+    logits = F.linear(hidden_states.float(), gate_weight.float(), None)
+    topk_indices, topk_weights, expert_counts = ops.moe_routing(logits, top_k)
+    expert_offsets = ops.moe_scan(expert_counts)
+    dispatched, token_map, dispatched_weights = ops.moe_dispatch(
+        hidden_states, topk_indices, topk_weights, expert_offsets)
+    if fuse_swiglu:
+        swiglu_out = ops.moe_gemm1_swiglu(dispatched, packed_w1, expert_offsets)
+    else:
+        swiglu_out = ops.swiglu(ops.moe_gemm1(dispatched, packed_w1, expert_offsets))
+    expert_out = ops.moe_gemm2(swiglu_out, w2, expert_offsets)
+    return ops.moe_combine(expert_out, token_map, dispatched_weights, T)
+
+
+class FusedMoELayer(nn.Module):
+    """Drop-in for DeepSeekMoE (moe.py:46-109; reference wrapper
+    moe_fused.py:161-216) that runs the fused device pipeline, shared expert
+    included. `moe_module` needs .gate.weight, .experts (gate_proj/up_proj/
+    down_proj each), .num_experts_per_tok and optionally .shared_experts."""
+
+    def __init__(self, moe_module: nn.Module, device: Optional[torch.device] = None):
+        super().__init__()
+        if not hasattr(moe_module, "gate") or not hasattr(moe_module, "experts"):
+            raise ValueError("FusedMoELayer: moe_module must have 'gate' and 'experts' attributes.")
+        dev = device if device is not None else moe_module.gate.weight.device
+        self.gate_weight = moe_module.gate.weight.detach().to(dev)
+        self.top_k = int(moe_module.num_experts_per_tok)
+        self.num_experts = len(moe_module.experts)
+        shared = getattr(moe_module, "shared_experts", None)
+        self.w1, self.w2, self.n_shared_groups = prepack_with_shared(
+            list(moe_module.experts), shared, device=dev)
+
+    def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
+        assert hidden_states.is_cuda, "hidden_states must be on CUDA."
+        assert hidden_states.dtype == torch.bfloat16, "hidden_states must be BF16."
+        orig = hidden_states.shape
+        x = hidden_states.reshape(-1, orig[-1]).contiguous()
+        logits = F.linear(x.float(), self.gate_weight.float(), None)
+        out = moe_fused_forward_logits(logits, x, self.w1, self.w2, self.top_k,
+                                       self.n_shared_groups, self.num_experts)
+        return out.view(orig)
+
+
+# id(experts) -> (packed_w1, w2), as the reference caches (moe_fused.py:224)
+_WEIGHT_CACHE: dict = {}
+
+
+def fused_moe_forward(hidden_states: torch.Tensor, gate_weight: torch.Tensor, experts: list,
+                      top_k: int = 6, packed_w1: Optional[torch.Tensor] = None,
+                      w2: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Functional form (moe_fused.py:227-272): routed experts only, like the
+    reference; weights are packed on first use and cached by id(experts)."""
+    assert hidden_states.is_cuda, "hidden_states must be on CUDA."
+    assert hidden_states.dim() == 2, "hidden_states must be [num_tokens, hidden_size]."
+    assert hidden_states.dtype == torch.bfloat16, "hidden_states must be BF16."
+    if packed_w1 is None or w2 is None:
+        key = id(experts)
+        if key not in _WEIGHT_CACHE:
+            _WEIGHT_CACHE[key] = prepack_experts(experts)
+        packed_w1, w2 = _WEIGHT_CACHE[key]
+    logits = F.linear(hidden_states.float(), gate_weight.float(), None)
+    return moe_fused_forward_logits(logits, hidden_states.contiguous(), packed_w1, w2, top_k, 0,
+                                    packed_w1.shape[0])

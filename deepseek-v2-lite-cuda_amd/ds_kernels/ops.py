@@ -1,0 +1,366 @@
+"""Torch-facing ops of ds_kernels: same names, argument order, defaults and
+return structure as the reference pybind module (src/kernels/bindings.cu:77-192).
+
+Every op checks its inputs the way the reference wrapper does (device, dtype,
+rank, contiguity: TORCH_CHECK -> RuntimeError), allocates its outputs and
+workspaces with the torch allocator on the input's device, and launches on
+torch's current stream through libdsk.so. There is no CPU path: CPU tensors are
+rejected, and a missing library fails at import.
+"""
+from __future__ import annotations
+
+from typing import List
+
+import torch
+
+from ._lib import check, lib, stream_handle
+
+MAX_EXPERTS = 64
+MAX_TOP_K = 6
+
+
+def _req(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _cuda_contig(t: torch.Tensor, name: str, op: str) -> None:
+    _req(isinstance(t, torch.Tensor), f"{op}: {name} must be a tensor.")
+    _req(t.is_cuda, f"{op}: {name} must reside on a CUDA device.")
+    _req(t.is_contiguous(), f"{op}: {name} must be contiguous in memory.")
+
+
+def _dtype(t: torch.Tensor, dt: torch.dtype, name: str, op: str) -> None:
+    _req(t.dtype == dt, f"{op}: {name} must be of type {str(dt).replace('torch.', '')}.")
+
+
+def _ws(nbytes: int, device: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+
+# ----------------------------------------------------------------- routing --
+def moe_routing(logits: torch.Tensor, top_k: int = 6) -> List[torch.Tensor]:
+    """Fused softmax + top-k routing (routing.cu:266-301).
+
+    logits fp32 [T, E] -> [topk_indices int32 [T,K], topk_weights fp32 [T,K],
+    expert_counts int32 [E]]. Ties go to the lower expert index; the k entries
+    are in descending weight order."""
+    op = "moe_routing"
+    _cuda_contig(logits, "logits", op)
+    _dtype(logits, torch.float32, "logits", op)
+    _req(logits.dim() == 2, f"{op}: logits must be a 2-D tensor [tokens, experts].")
+    T, E = logits.shape
+    _req(E <= MAX_EXPERTS, "num_experts must not exceed 64.")
+    _req(top_k <= MAX_TOP_K, "top_k must not exceed 6.")
+    _req(top_k >= 1 and top_k <= E, f"{op}: top_k must be in [1, num_experts].")
+    dev = logits.device
+    idx = torch.empty((T, top_k), dtype=torch.int32, device=dev)
+    w = torch.empty((T, top_k), dtype=torch.float32, device=dev)
+    counts = torch.empty((E,), dtype=torch.int32, device=dev)
+    nws = lib.dsk_moe_routing_workspace_size(T, E)
+    ws = _ws(nws, dev)
+    with torch.cuda.device(dev):
+        check(lib.dsk_moe_routing(logits.data_ptr(), E, idx.data_ptr(), w.data_ptr(),
+                                  counts.data_ptr(), T, E, top_k, ws.data_ptr(), ws.numel(),
+                                  stream_handle(dev)), op)
+    return [idx, w, counts]
+
+
+def moe_scan(expert_counts: torch.Tensor) -> torch.Tensor:
+    """Exclusive prefix sum with sentinel (scan.cu:86-130), entirely on the device."""
+    op = "moe_scan"
+    _cuda_contig(expert_counts, "expert_counts", op)
+    _dtype(expert_counts, torch.int32, "expert_counts", op)
+    _req(expert_counts.dim() == 1, f"{op}: expert_counts must be a 1-D tensor [num_experts].")
+    E = expert_counts.shape[0]
+    _req(1 <= E <= MAX_EXPERTS, f"{op}: num_experts must be in [1, 64].")
+    dev = expert_counts.device
+    offsets = torch.empty((E + 1,), dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        check(lib.dsk_moe_scan(expert_counts.data_ptr(), offsets.data_ptr(), E,
+                               stream_handle(dev)), op)
+    return offsets
+
+
+def moe_dispatch(input: torch.Tensor, topk_indices: torch.Tensor, topk_weights: torch.Tensor,
+                 expert_offsets: torch.Tensor) -> List[torch.Tensor]:
+    """Stable dispatch (dispatch.cu:156-218): expert-major slots, ascending token
+    order inside an expert. -> [dispatched bf16 [S,H], token_map int32 [S],
+    dispatched_weights fp32 [S]] with S = T * top_k."""
+    op = "moe_dispatch"
+    _cuda_contig(input, "input", op)
+    _dtype(input, torch.bfloat16, "input", op)
+    _req(input.dim() == 2, f"{op}: input must be a 2-D tensor [num_tokens, hidden_size].")
+    _cuda_contig(topk_indices, "topk_indices", op)
+    _dtype(topk_indices, torch.int32, "topk_indices", op)
+    _req(topk_indices.dim() == 2, f"{op}: topk_indices must be a 2-D tensor [num_tokens, top_k].")
+    _cuda_contig(topk_weights, "topk_weights", op)
+    _dtype(topk_weights, torch.float32, "topk_weights", op)
+    _req(topk_weights.dim() == 2, f"{op}: topk_weights must be a 2-D tensor [num_tokens, top_k].")
+    _cuda_contig(expert_offsets, "expert_offsets", op)
+    _dtype(expert_offsets, torch.int32, "expert_offsets", op)
+    _req(expert_offsets.dim() == 1, f"{op}: expert_offsets must be a 1-D tensor [num_experts + 1].")
+    T, H = input.shape
+    K = topk_indices.shape[1]
+    E = expert_offsets.shape[0] - 1
+    _req(topk_indices.shape[0] == T and tuple(topk_weights.shape) == (T, K),
+         f"{op}: topk_indices/topk_weights must be [num_tokens, top_k].")
+    _req(H % 8 == 0, "hidden_size must be divisible by 8 for 128-bit vectorized access.")
+    _req(1 <= E <= MAX_EXPERTS, f"{op}: num_experts must be in [1, 64].")
+    _req(1 <= K <= MAX_TOP_K, f"{op}: top_k must be in [1, 6].")
+    dev = input.device
+    S = T * K
+    dispatched = torch.empty((S, H), dtype=torch.bfloat16, device=dev)
+    token_map = torch.empty((S,), dtype=torch.int32, device=dev)
+    dw = torch.empty((S,), dtype=torch.float32, device=dev)
+    ws = _ws(lib.dsk_moe_dispatch_workspace_size(T, E, K), dev)
+    with torch.cuda.device(dev):
+        check(lib.dsk_moe_dispatch(input.data_ptr(), H, topk_indices.data_ptr(),
+                                   topk_weights.data_ptr(), expert_offsets.data_ptr(),
+                                   dispatched.data_ptr(), token_map.data_ptr(), dw.data_ptr(),
+                                   T, H, E, K, ws.data_ptr(), ws.numel(), stream_handle(dev)), op)
+    return [dispatched, token_map, dw]
+
+
+def moe_combine(expert_output: torch.Tensor, token_map: torch.Tensor,
+                dispatched_weights: torch.Tensor, num_tokens: int) -> torch.Tensor:
+    """Deterministic weighted combine (combine.cu:107-176): for every token, the
+    slots that map to it are summed in ascending slot order in fp32 and rounded
+    to bf16 once. No float atomics."""
+    op = "moe_combine"
+    _cuda_contig(expert_output, "expert_output", op)
+    _dtype(expert_output, torch.bfloat16, "expert_output", op)
+    _req(expert_output.dim() == 2, f"{op}: expert_output must be a 2-D tensor [total_slots, hidden_size].")
+    _cuda_contig(token_map, "token_map", op)
+    _dtype(token_map, torch.int32, "token_map", op)
+    _req(token_map.dim() == 1, f"{op}: token_map must be a 1-D tensor [total_slots].")
+    _cuda_contig(dispatched_weights, "dispatched_weights", op)
+    _dtype(dispatched_weights, torch.float32, "dispatched_weights", op)
+    _req(dispatched_weights.dim() == 1, f"{op}: dispatched_weights must be a 1-D tensor [total_slots].")
+    S, H = expert_output.shape
+    _req(token_map.shape[0] == S and dispatched_weights.shape[0] == S,
+         f"{op}: token_map/dispatched_weights must have total_slots entries.")
+    _req(int(num_tokens) > 0, "num_tokens must be positive.")
+    _req(H % 8 == 0, f"{op}: hidden_size must be divisible by 8.")
+    dev = expert_output.device
+    out = torch.empty((int(num_tokens), H), dtype=torch.bfloat16, device=dev)
+    ws = _ws(lib.dsk_moe_combine_workspace_size(S, int(num_tokens)), dev)
+    with torch.cuda.device(dev):
+        check(lib.dsk_moe_combine(expert_output.data_ptr(), token_map.data_ptr(),
+                                  dispatched_weights.data_ptr(), out.data_ptr(), S,
+                                  int(num_tokens), H, ws.data_ptr(), ws.numel(),
+                                  stream_handle(dev)), op)
+    return out
+
+
+def swiglu(input: torch.Tensor) -> torch.Tensor:
+    """silu(input[:, :I]) * input[:, I:] (swiglu.cu:142-170)."""
+    op = "swiglu"
+    _req(input.is_cuda, f"{op}: input must be a CUDA tensor.")
+    _req(input.is_contiguous(), f"{op}: input must be contiguous.")
+    _req(input.dtype == torch.bfloat16, f"{op}: input must be bfloat16.")
+    _req(input.dim() == 2, f"{op}: input must be 2-D [total_tokens, 2*intermediate_size].")
+    _req(input.shape[1] % 2 == 0, f"{op}: input inner dimension must be even.")
+    rows, n2 = input.shape
+    I = n2 // 2
+    out = torch.empty((rows, I), dtype=torch.bfloat16, device=input.device)
+    with torch.cuda.device(input.device):
+        check(lib.dsk_swiglu(input.data_ptr(), out.data_ptr(), rows, I,
+                             stream_handle(input.device)), op)
+    return out
+
+
+def _gemm_checks(op: str, a: torch.Tensor, aname: str, w: torch.Tensor, wname: str,
+                 offsets: torch.Tensor) -> None:
+    _req(a.is_cuda and a.is_contiguous(), f"{op}: {aname} must be a contiguous CUDA tensor.")
+    _req(a.dtype == torch.bfloat16, f"{op}: {aname} must be bfloat16.")
+    _req(a.dim() == 2, f"{op}: {aname} must be 2-D.")
+    _req(w.is_cuda and w.is_contiguous(), f"{op}: {wname} must be a contiguous CUDA tensor.")
+    _req(w.dtype == torch.bfloat16, f"{op}: {wname} must be bfloat16.")
+    _req(w.dim() == 3, f"{op}: {wname} must be 3-D [num_experts, out, in].")
+    _req(offsets.is_cuda and offsets.is_contiguous(),
+         f"{op}: expert_offsets must be a contiguous CUDA tensor.")
+    _req(offsets.dtype == torch.int32, f"{op}: expert_offsets must be int32.")
+    _req(offsets.dim() == 1, f"{op}: expert_offsets must be 1-D [num_experts + 1].")
+    _req(w.shape[2] == a.shape[1], f"{op}: {wname} inner dim does not match {aname}.")
+    _req(offsets.shape[0] == w.shape[0] + 1, f"{op}: expert_offsets size must be num_experts + 1.")
+
+
+def moe_gemm1(dispatched: torch.Tensor, packed_w1: torch.Tensor,
+              expert_offsets: torch.Tensor) -> torch.Tensor:
+    """Grouped gate|up projection (gemm1.cu:167-227): out[s] = dispatched[s] @
+    packed_w1[e]^T for s in expert e's offset range; uncovered rows are zero."""
+    op = "gemm1"
+    _gemm_checks(op, dispatched, "dispatched", packed_w1, "packed_w1", expert_offsets)
+    S, H = dispatched.shape
+    E, N, _ = packed_w1.shape
+    out = torch.empty((S, N), dtype=torch.bfloat16, device=dispatched.device)
+    if S == 0:
+        return out
+    with torch.cuda.device(dispatched.device):
+        check(lib.dsk_moe_gemm1(dispatched.data_ptr(), packed_w1.data_ptr(), out.data_ptr(),
+                                expert_offsets.data_ptr(), S, E, H, N,
+                                stream_handle(dispatched.device)), op)
+    return out
+
+
+def moe_gemm1_swiglu(dispatched: torch.Tensor, packed_w1: torch.Tensor,
+                     expert_offsets: torch.Tensor) -> torch.Tensor:
+    """moe_gemm1 followed by swiglu, fused: SwiGLU is applied to the fp32
+    accumulators in the GEMM epilogue. -> [S, I] bf16."""
+    op = "gemm1_swiglu"
+    _gemm_checks(op, dispatched, "dispatched", packed_w1, "packed_w1", expert_offsets)
+    S, H = dispatched.shape
+    E, N, _ = packed_w1.shape
+    _req(N % 2 == 0, f"{op}: packed_w1 rows must be 2*intermediate.")
+    I = N // 2
+    out = torch.empty((S, I), dtype=torch.bfloat16, device=dispatched.device)
+    if S == 0:
+        return out
+    with torch.cuda.device(dispatched.device):
+        check(lib.dsk_moe_gemm1_swiglu(dispatched.data_ptr(), packed_w1.data_ptr(),
+                                       out.data_ptr(), expert_offsets.data_ptr(), S, E, H, I,
+                                       stream_handle(dispatched.device)), op)
+    return out
+
+
+def moe_gemm2(swiglu_out: torch.Tensor, w2: torch.Tensor,
+              expert_offsets: torch.Tensor) -> torch.Tensor:
+    """Grouped down projection (gemm2.cu:136-195)."""
+    op = "gemm2"
+    _gemm_checks(op, swiglu_out, "swiglu_out", w2, "w2", expert_offsets)
+    S, I = swiglu_out.shape
+    E, H, _ = w2.shape
+    out = torch.empty((S, H), dtype=torch.bfloat16, device=swiglu_out.device)
+    if S == 0:
+        return out
+    with torch.cuda.device(swiglu_out.device):
+        check(lib.dsk_moe_gemm2(swiglu_out.data_ptr(), w2.data_ptr(), out.data_ptr(),
+                                expert_offsets.data_ptr(), S, E, I, H,
+                                stream_handle(swiglu_out.device)), op)
+    return out
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """x[..., K] @ weight[N, K]^T with the MFMA GEMM (bf16 in/out, fp32 acc).
+    x may be a row-strided view (last dim contiguous, row stride % 8 == 0)."""
+    op = "linear"
+    _req(x.is_cuda and weight.is_cuda, f"{op}: tensors must be CUDA tensors.")
+    _req(x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16, f"{op}: bfloat16 only.")
+    _req(weight.dim() == 2 and weight.is_contiguous(), f"{op}: weight must be contiguous 2-D.")
+    K = x.shape[-1]
+    N = weight.shape[0]
+    _req(weight.shape[1] == K, f"{op}: weight inner dim {weight.shape[1]} != {K}.")
+    x2 = x.reshape(-1, K) if not x.is_contiguous() or x.dim() != 2 else x
+    _req(x2.stride(-1) == 1, f"{op}: last dim of x must be contiguous.")
+    M = x2.shape[0]
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    if M:
+        with torch.cuda.device(x.device):
+            check(lib.dsk_linear(x2.data_ptr(), x2.stride(0), weight.data_ptr(), out.data_ptr(),
+                                 N, M, K, N, stream_handle(x.device)), op)
+    return out.view(*x.shape[:-1], N)
+
+
+def kv_upproj(normed_kv: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """kv_b_proj up-projection (kv_upproj.cu:133-178): [..., 512] -> [..., out_dim]."""
+    op = "kv_upproj"
+    _req(normed_kv.is_cuda and normed_kv.is_contiguous(),
+         f"{op}: normed_kv must be a contiguous CUDA tensor.")
+    _req(normed_kv.dtype == torch.bfloat16, f"{op}: normed_kv must be bfloat16.")
+    _req(normed_kv.dim() >= 2, f"{op}: normed_kv must have at least 2 dimensions.")
+    _req(weight.is_cuda and weight.is_contiguous(), f"{op}: weight must be a contiguous CUDA tensor.")
+    _req(weight.dtype == torch.bfloat16, f"{op}: weight must be bfloat16.")
+    _req(weight.dim() == 2, f"{op}: weight must be 2-D [out_dim, kv_lora_rank].")
+    r = normed_kv.shape[-1]
+    _req(weight.shape[1] == r,
+         f"{op}: weight inner dim {weight.shape[1]} must match normed_kv last dim {r}.")
+    n = weight.shape[0]
+    rows = normed_kv.numel() // r
+    out = torch.empty((*normed_kv.shape[:-1], n), dtype=torch.bfloat16, device=normed_kv.device)
+    if rows:
+        with torch.cuda.device(normed_kv.device):
+            check(lib.dsk_kv_upproj(normed_kv.data_ptr(), r, weight.data_ptr(), out.data_ptr(),
+                                    rows, r, n, stream_handle(normed_kv.device)), op)
+    return out
+
+
+def rms_norm(input: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """RMSNorm over the last dim (rms_norm.cu:158-192): bf16 input, fp32 weight,
+    bf16 output. An fp32 input selects the fp32-in/fp32-out kernel. The input may
+    be a row-strided view (last dim contiguous), e.g. the latent slice of kv_a."""
+    op = "rms_norm"
+    _req(input.is_cuda, f"{op}: input must be a CUDA tensor.")
+    _req(weight.is_cuda, f"{op}: weight must be a CUDA tensor.")
+    _req(input.dtype in (torch.bfloat16, torch.float32), f"{op}: input must be bfloat16.")
+    _req(weight.dtype == torch.float32,
+         f"{op}: weight must be float32 (default nn.Parameter dtype).")
+    _req(input.dim() >= 2, f"{op}: input must have at least 2 dimensions.")
+    H = input.shape[-1]
+    _req(weight.numel() == H,
+         f"{op}: weight size {weight.numel()} does not match input hidden_size {H}.")
+    weight = weight.contiguous()
+    if input.dtype == torch.bfloat16:
+        _req(H % 2 == 0, f"{op}: hidden_size must be even for bfloat162 vectorisation.")
+    # Flatten leading dims without a copy when the rows are uniformly strided.
+    try:
+        x2 = input.view(-1, H)
+    except RuntimeError:
+        x2 = None
+    if x2 is None or x2.stride(-1) != 1:
+        x2 = input.contiguous().view(-1, H)
+    rows = x2.shape[0]
+    out = torch.empty(input.shape, dtype=input.dtype, device=input.device)
+    if rows == 0:
+        return out
+    fn = lib.dsk_rms_norm if input.dtype == torch.bfloat16 else lib.dsk_rms_norm_f32
+    with torch.cuda.device(input.device):
+        check(fn(x2.data_ptr(), x2.stride(0), weight.data_ptr(), out.data_ptr(), H, rows, H,
+                 float(eps), stream_handle(input.device)), op)
+    return out
+
+
+def _rope_strides(t: torch.Tensor, name: str):
+    _req(t.dim() == 4, f"rope: {name} must be 4-D.")
+    _req(t.stride(3) == 1, f"rope: {name} last dim must be contiguous.")
+    b, h, s, d = t.shape
+    sb, sh, ss = t.stride(0), t.stride(1), t.stride(2)
+    return sb, (sh if h > 1 else 0), ss
+
+
+def rope(q_pe: torch.Tensor, k_pe: torch.Tensor, cos: torch.Tensor,
+         sin: torch.Tensor) -> List[torch.Tensor]:
+    """Interleaved -> half RoPE on q_pe [b,h,s,d] and k_pe [b,1,s,d] with the
+    pre-indexed cos/sin [b,1,s,d] (rope.cu:139-207). Inputs may be strided
+    views (last dim contiguous); outputs are contiguous."""
+    op = "rope"
+    for t, n in ((q_pe, "q_pe"), (k_pe, "k_pe"), (cos, "cos"), (sin, "sin")):
+        _req(t.is_cuda, f"{op}: all inputs must be CUDA tensors.")
+        _req(t.dtype == torch.bfloat16, f"{op}: all inputs must be bfloat16.")
+    _req(q_pe.dim() == 4, f"{op}: q_pe must be 4-D [bsz, heads, seq, rope_dim].")
+    _req(k_pe.dim() == 4, f"{op}: k_pe must be 4-D [bsz, 1, seq, rope_dim].")
+    _req(cos.dim() == 4, f"{op}: cos must be 4-D [bsz, 1, seq, rope_dim].")
+    _req(sin.dim() == 4, f"{op}: sin must be 4-D [bsz, 1, seq, rope_dim].")
+    b, hq, s, d = q_pe.shape
+    _req(k_pe.shape[0] == b and k_pe.shape[2] == s and k_pe.shape[3] == d,
+         f"{op}: k_pe shape {list(k_pe.shape)} incompatible with q_pe.")
+    _req(cos.shape[0] == b and cos.shape[2] == s and cos.shape[3] == d,
+         f"{op}: cos shape incompatible.")
+    _req(sin.shape[0] == b and sin.shape[2] == s and sin.shape[3] == d,
+         f"{op}: sin shape incompatible.")
+    _req(d % 2 == 0, f"{op}: rope_dim must be even.")
+    _req(d % 8 == 0, f"{op}: rope_dim must be a multiple of 8.")
+    if cos.stride(3) != 1 or sin.stride(3) != 1 or cos.stride() != sin.stride():
+        cos, sin = cos.contiguous(), sin.contiguous()
+    cb, cs = cos.stride(0), cos.stride(2)
+    qsb, qsh, qss = _rope_strides(q_pe, "q_pe")
+    ksb, ksh, kss = _rope_strides(k_pe, "k_pe")
+    hk = k_pe.shape[1]
+    q_rot = torch.empty((b, hq, s, d), dtype=torch.bfloat16, device=q_pe.device)
+    k_rot = torch.empty((b, hk, s, d), dtype=torch.bfloat16, device=q_pe.device)
+    with torch.cuda.device(q_pe.device):
+        check(lib.dsk_rope_qk(q_pe.data_ptr(), qsb, qsh, qss, k_pe.data_ptr(), ksb, ksh, kss,
+                              cos.data_ptr(), sin.data_ptr(), cb, cs, q_rot.data_ptr(),
+                              k_rot.data_ptr(), b, hq, hk, s, d,
+                              stream_handle(q_pe.device)), op)
+    return [q_rot, k_rot]

@@ -1,0 +1,214 @@
+/*
+ * dsk.h — C ABI of libdsk.so, the gfx950 (MI355X) implementation of the
+ * DeepSeek-V2-Lite fused MoE layer and its MLA helper kernels.
+ *
+ * Every entry point:
+ *   - takes raw device pointers, explicit sizes/row strides and the HIP stream
+ *     as its LAST argument (a hipStream_t passed as void*; NULL = default stream);
+ *   - never allocates or frees device memory: outputs and workspaces are
+ *     allocated by the caller (workspace sizes come from the *_workspace_size
+ *     queries);
+ *   - returns 0 on success, or a nonzero DSK_ERR_* code, in which case
+ *     dsk_last_error() returns a thread-local message. Launch errors are
+ *     checked with hipGetLastError() after every kernel launch.
+ *   - never synchronises with the host: expert offsets stay on the device and
+ *     the GEMM tile schedulers read them there.
+ *
+ * bf16 tensors are passed as dsk_bf16 (raw 16-bit storage, round-to-nearest-even).
+ * Each declaration cites the reference interface it replaces
+ * (sahan974/DeepSeek-V2-Lite-CUDA, file:line).
+ */
+#ifndef DSK_H_
+#define DSK_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint16_t dsk_bf16;
+
+enum {
+  DSK_OK = 0,
+  DSK_ERR_INVALID_ARG = 1,   /* shape / size / limit violation            */
+  DSK_ERR_NULL_PTR = 2,      /* a required pointer is NULL                 */
+  DSK_ERR_ALIGNMENT = 3,     /* pointer or stride not 16-byte aligned      */
+  DSK_ERR_LAUNCH = 4,        /* hipGetLastError() reported a launch error  */
+  DSK_ERR_WORKSPACE = 5      /* workspace too small                        */
+};
+
+/* Limits mirrored from the reference routing kernel (routing.cu:32-33). */
+#define DSK_MAX_EXPERTS 64
+#define DSK_MAX_TOP_K 6
+
+/* Thread-local message describing the last failed call on this thread. */
+const char* dsk_last_error(void);
+/* ABI version of this library (bumped on any signature change). */
+int dsk_abi_version(void);
+
+/* ---------------------------------------------------------------- routing --
+ * Softmax over E expert logits + top-K (ties -> lower expert index, emitted in
+ * descending-weight order) + per-expert counts.
+ * Replaces launch_moe_routing (include/moe/routing.h:27-36, routing.cu:230-260)
+ * and moe_routing_forward (routing.cu:266-301). logits: fp32 [T, E] with row
+ * stride ld_logits (elements); topk_idx int32 [T,K]; topk_w fp32 [T,K];
+ * expert_counts int32 [E]. E <= 64, K <= 6, K <= E. */
+size_t dsk_moe_routing_workspace_size(int num_tokens, int num_experts);
+int dsk_moe_routing(const float* logits, int64_t ld_logits, int32_t* topk_idx,
+                    float* topk_w, int32_t* expert_counts, int num_tokens,
+                    int num_experts, int top_k, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------- scan --
+ * expert_offsets[0] = 0, expert_offsets[e+1] = expert_offsets[e] + counts[e];
+ * expert_offsets[E] = total. Computed on the device (no host round trip).
+ * Replaces launch_moe_scan (include/moe/scan.h:31-36, scan.cu:33-75) and
+ * moe_scan_forward (scan.cu:86-130). */
+int dsk_moe_scan(const int32_t* expert_counts, int32_t* expert_offsets,
+                 int num_experts, void* stream);
+
+/* --------------------------------------------------------------- dispatch --
+ * Deterministic, stable dispatch: slot s in [offsets[e], offsets[e+1]) holds
+ * the tokens routed to expert e in ascending token order.
+ *   token_map[s] = t, dispatched_weights[s] = topk_w[t,k], dispatched[s,:] = x[t,:]
+ * x: bf16 [T, H] with row stride ld_x (H % 8 == 0, 16-byte aligned rows).
+ * dispatched may be NULL (index-only dispatch). Entries whose expert index is
+ * outside [0,E) or whose slot falls outside [0, T*K) are skipped.
+ * Replaces launch_moe_dispatch (include/moe/dispatch.h:44-57,
+ * dispatch.cu:106-139) and moe_dispatch_forward (dispatch.cu:156-218). */
+size_t dsk_moe_dispatch_workspace_size(int num_tokens, int num_experts,
+                                       int top_k);
+int dsk_moe_dispatch(const dsk_bf16* x, int64_t ld_x, const int32_t* topk_idx,
+                     const float* topk_w, const int32_t* expert_offsets,
+                     dsk_bf16* dispatched, int32_t* token_map,
+                     float* dispatched_weights, int num_tokens, int hidden,
+                     int num_experts, int top_k, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------- combine --
+ * out[t,:] = bf16( sum over slots s with token_map[s]==t, in ascending s, of
+ *                  dispatched_weights[s] * float(expert_out[s,:]) ), fp32
+ * accumulation, one rounding, no float atomics. Tokens with no slot -> 0.
+ * Replaces launch_moe_combine (include/moe/combine.h:41-49, combine.cu:80-93)
+ * and moe_combine_forward (combine.cu:107-176). */
+size_t dsk_moe_combine_workspace_size(int total_slots, int num_tokens);
+int dsk_moe_combine(const dsk_bf16* expert_out, const int32_t* token_map,
+                    const float* dispatched_weights, dsk_bf16* out,
+                    int total_slots, int num_tokens, int hidden,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* ----------------------------------------------------------------- swiglu --
+ * out[s, j] = bf16( silu(in[s, j]) * in[s, I + j] ), fp32 math.
+ * Replaces launch_swiglu (include/moe/swiglu.h:26-32, swiglu.cu:114-130). */
+int dsk_swiglu(const dsk_bf16* in, dsk_bf16* out, int rows,
+               int intermediate, void* stream);
+
+/* ------------------------------------------------------------ grouped GEMM --
+ * gemm1: out[s, :] = dispatched[s, :] @ packed_w1[e]^T for s in
+ * [offsets[e], offsets[e+1]); rows outside [offsets[0], offsets[E]) are zero.
+ * packed_w1: [E, N, H] (N = 2*I, gate rows then up rows); out [S, N].
+ * Offsets are read on the device and clamped to [0, S].
+ * Replaces launch_moe_gemm1 (include/moe/gemm1.h:25-34, gemm1.cu:84-155) and
+ * moe_gemm1_forward (gemm1.cu:167-227). */
+int dsk_moe_gemm1(const dsk_bf16* dispatched, const dsk_bf16* packed_w1,
+                  dsk_bf16* out, const int32_t* expert_offsets,
+                  int total_slots, int num_experts, int hidden, int n_out,
+                  void* stream);
+
+/* gemm1 + SwiGLU fused in the epilogue: out[s, j] = silu(g) * u with
+ * g = x.W1[e][j], u = x.W1[e][I + j] (fp32 accumulators, one rounding).
+ * out: [S, I]. No reference counterpart as one op: it is moe_gemm1 followed by
+ * swiglu (moe_fused.py:103-106). */
+int dsk_moe_gemm1_swiglu(const dsk_bf16* dispatched,
+                         const dsk_bf16* packed_w1, dsk_bf16* out,
+                         const int32_t* expert_offsets, int total_slots,
+                         int num_experts, int hidden, int intermediate,
+                         void* stream);
+
+/* gemm2: out[s, :] = swiglu_out[s, :] @ w2[e]^T; w2: [E, H, I]; out [S, H].
+ * Replaces launch_moe_gemm2 (include/moe/gemm2.h:25-34, gemm2.cu:75-124) and
+ * moe_gemm2_forward (gemm2.cu:136-195). */
+int dsk_moe_gemm2(const dsk_bf16* swiglu_out, const dsk_bf16* w2,
+                  dsk_bf16* out, const int32_t* expert_offsets,
+                  int total_slots, int num_experts, int intermediate,
+                  int hidden, void* stream);
+
+/* Dense linear out[M, N] = x[M, K] @ w[N, K]^T (bf16 in/out, fp32 accumulate),
+ * x row stride ld_x, out row stride ld_out (elements, multiples of 8).
+ * kv_upproj is this op with K = kv_lora_rank (512), N = 4096.
+ * Replaces launch_kv_upproj (include/mla/kv_upproj.h:31-39,
+ * kv_upproj.cu:77-119) and kv_upproj_forward (kv_upproj.cu:133-178). */
+int dsk_linear(const dsk_bf16* x, int64_t ld_x, const dsk_bf16* w,
+               dsk_bf16* out, int64_t ld_out, int M, int K, int N,
+               void* stream);
+int dsk_kv_upproj(const dsk_bf16* normed_kv, int64_t ld_in,
+                  const dsk_bf16* weight, dsk_bf16* out, int rows,
+                  int kv_lora_rank, int out_dim, void* stream);
+
+/* --------------------------------------------------------------- rms_norm --
+ * y = w * x * rsqrt(mean(x^2) + eps), fp32 math, one rounding of the output.
+ * bf16 in/out with fp32 weight: replaces launch_rms_norm
+ * (include/mla/rms_norm.h:26-34, rms_norm.cu:126-144) and rms_norm_forward
+ * (rms_norm.cu:158-192). Row strides allow normalising a strided view (e.g. the
+ * 512-wide latent inside the 576-wide kv_a output) without a copy.
+ * The _f32 variant is fp32 in/out (the 1e-5 path of RMSNorm, mla.py:53-64). */
+int dsk_rms_norm(const dsk_bf16* in, int64_t ld_in, const float* weight,
+                 dsk_bf16* out, int64_t ld_out, int rows, int hidden,
+                 float eps, void* stream);
+int dsk_rms_norm_f32(const float* in, int64_t ld_in, const float* weight,
+                     float* out, int64_t ld_out, int rows, int hidden,
+                     float eps, void* stream);
+
+/* ------------------------------------------------------------------- rope --
+ * Interleaved-to-half rotary embedding (mla.py:176-206, rope.cu:61-95):
+ *   out[k]      = x[2k]   * cos[k]      - x[2k+1] * sin[k]
+ *   out[k+d/2]  = x[2k+1] * cos[k+d/2]  + x[2k]   * sin[k+d/2]
+ * x viewed as [B, Hh, S, d] with element strides (sb, sh, ss), last dim
+ * contiguous; cos/sin are the pre-indexed tables [B, 1, S, d] with strides
+ * (cb, cs), broadcast over heads (no materialised copy). out is contiguous
+ * [B, Hh, S, d]. d must be a multiple of 8 and <= 256.
+ * Replaces launch_rope (include/mla/rope.h:30-38, rope.cu:101-119) and
+ * rope_forward (rope.cu:139-207); dsk_rope_qk does q and k in one launch. */
+int dsk_rope(const dsk_bf16* x, int64_t sb, int64_t sh, int64_t ss,
+             const dsk_bf16* cos_t, const dsk_bf16* sin_t, int64_t cb,
+             int64_t cs, dsk_bf16* out, int B, int Hh, int S, int d,
+             void* stream);
+int dsk_rope_qk(const dsk_bf16* q, int64_t qsb, int64_t qsh, int64_t qss,
+                const dsk_bf16* k, int64_t ksb, int64_t ksh, int64_t kss,
+                const dsk_bf16* cos_t, const dsk_bf16* sin_t, int64_t cb,
+                int64_t cs, dsk_bf16* q_out, dsk_bf16* k_out, int B, int Hq,
+                int Hk, int S, int d, void* stream);
+
+/* ------------------------------------------------------- fused MoE layer --
+ * The whole DeepSeekMoE forward (moe.py:77-109) on the device:
+ *   route -> stable permutation -> grouped GEMM1+SwiGLU -> grouped GEMM2 ->
+ *   deterministic combine (+ shared expert), with no host synchronisation.
+ * logits: fp32 [T, E] (gate GEMM output, as moe_fused.py:131 computes it);
+ * x: bf16 [T, H]; w1: bf16 [G, 2I, H] and w2: bf16 [G, H, I] where
+ * G = E + n_shared_groups. Groups E.. are the shared expert split into
+ * n_shared_groups slices of width I (every token routes to them with weight
+ * 1.0). out: bf16 [T, H]. The replaced reference caller is
+ * _route_dispatch_combine (moe_fused.py:118-154), which omits shared experts.
+ * Optional debug outputs (may be NULL): topk_idx [T,K], topk_w [T,K],
+ * expert_offsets [E+1]. Optional instrumentation (may be NULL): stage_events
+ * points to 5 hipEvent_t recorded on `stream` before routing, after the
+ * permutation, after GEMM1+SwiGLU, after GEMM2 and after the combine. */
+size_t dsk_moe_fused_workspace_size(int num_tokens, int num_experts,
+                                    int top_k, int n_shared_groups,
+                                    int hidden, int intermediate);
+int dsk_moe_fused_forward(const float* logits, const dsk_bf16* x,
+                          const dsk_bf16* w1, const dsk_bf16* w2,
+                          dsk_bf16* out, int num_tokens, int num_experts,
+                          int top_k, int n_shared_groups, int hidden,
+                          int intermediate, int32_t* topk_idx_out,
+                          float* topk_w_out, int32_t* expert_offsets_out,
+                          void* workspace, size_t workspace_bytes,
+                          void* const* stage_events, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSK_H_ */

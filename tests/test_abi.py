@@ -1,0 +1,107 @@
+"""C-ABI checks that need no GPU: libdsk.so loads, exports every function
+declared in include/dsk.h, and rejects bad arguments with a status code and a
+message before touching the device (reference error behaviour: TORCH_CHECK /
+std::runtime_error -> RuntimeError)."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "dsk.h")
+
+
+def declared_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(dsk_[a-z0-9_]+)\s*\(", src)))
+
+
+@pytest.fixture(scope="module")
+def dsk():
+    import ds_kernels
+    return ds_kernels
+
+
+def test_every_declared_symbol_is_exported(dsk):
+    names = declared_functions()
+    assert len(names) >= 20
+    raw = ctypes.CDLL(dsk.LIB_PATH)
+    missing = [n for n in names if not hasattr(raw, n)]
+    assert not missing, f"not exported: {missing}"
+    from ds_kernels._lib import SIGNATURES
+    assert set(names) == set(SIGNATURES), "python binding out of sync with include/dsk.h"
+
+
+def test_abi_version(dsk):
+    assert dsk.lib.dsk_abi_version() == 1
+
+
+def _err(dsk):
+    return dsk.lib.dsk_last_error().decode()
+
+
+def test_routing_limits_rejected(dsk):
+    lib = dsk.lib
+    rc = lib.dsk_moe_routing(None, 65, None, None, 8, 4, 65, 6, None, 0, None)
+    assert rc == 1 and "num_experts" in _err(dsk)
+    rc = lib.dsk_moe_routing(None, 64, None, None, 8, 4, 64, 7, None, 0, None)
+    assert rc == 1 and "top_k" in _err(dsk)
+    rc = lib.dsk_moe_routing(None, 64, None, None, None, 4, 64, 6, None, 0, None)
+    assert rc == 2
+
+
+def test_dispatch_and_combine_validation(dsk):
+    lib = dsk.lib
+    rc = lib.dsk_moe_dispatch(None, 2044, None, None, None, None, None, None, 4, 2044, 64, 6,
+                              None, 0, None)
+    assert rc == 1 and "divisible by 8" in _err(dsk)
+    rc = lib.dsk_moe_combine(None, None, None, None, 6, 0, 2048, None, 0, None)
+    assert rc == 1 and "num_tokens must be positive" in _err(dsk)
+
+
+def test_gemm_validation(dsk):
+    lib = dsk.lib
+    # K not a multiple of 64
+    rc = lib.dsk_moe_gemm1(16, 16, 16, 16, 6, 64, 100, 2816, None)
+    assert rc == 1 and "multiple of 64" in _err(dsk)
+    # misaligned pointers
+    rc = lib.dsk_moe_gemm2(18, 16, 16, 16, 6, 64, 1408, 2048, None)
+    assert rc == 3
+    # too many groups
+    rc = lib.dsk_moe_gemm2(16, 16, 16, 16, 6, 200, 1408, 2048, None)
+    assert rc == 1
+
+
+def test_norm_rope_validation(dsk):
+    lib = dsk.lib
+    rc = lib.dsk_rms_norm(16, 511, 16, 16, 511, 4, 511, 1e-6, None)
+    assert rc == 1 and "even" in _err(dsk)
+    rc = lib.dsk_rope(16, 0, 0, 64, 16, 16, 0, 64, 16, 1, 1, 4, 60, None)
+    assert rc == 1
+
+
+def test_fused_validation_and_workspace_sizes(dsk):
+    lib = dsk.lib
+    assert lib.dsk_moe_fused_workspace_size(4096, 64, 6, 2, 2048, 1408) > \
+        (4096 * 8) * (2048 + 1408) * 2
+    assert lib.dsk_moe_dispatch_workspace_size(100, 64, 6) >= 2 * 100 * 6 * 4
+    assert lib.dsk_moe_combine_workspace_size(600, 100) >= (2 * 101 + 2 * 600) * 4
+    rc = lib.dsk_moe_fused_forward(None, None, None, None, None, 4, 64, 6, 2, 2048, 1400, None,
+                                   None, None, None, 0, None, None)
+    assert rc == 1
+    rc = lib.dsk_moe_fused_forward(16, 16, 16, 16, 16, 4, 64, 6, 2, 2048, 1408, None, None, None,
+                                   None, 0, None, None)
+    assert rc == 5 and "workspace" in _err(dsk)
+
+
+def test_python_ops_reject_cpu_tensors(dsk):
+    logits = torch.zeros(4, 64)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        dsk.moe_routing(logits, 6)
+    with pytest.raises(RuntimeError):
+        dsk.moe_scan(torch.zeros(64, dtype=torch.int32))
+    with pytest.raises(RuntimeError):
+        dsk.rms_norm(torch.zeros(2, 8, dtype=torch.bfloat16), torch.ones(8))

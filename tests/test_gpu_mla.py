@@ -1,0 +1,104 @@
+"""GPU parity of the MLA helper kernels (rms_norm, rope, kv_upproj) and the
+dense MFMA linear against the numpy oracle."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import BF16_TOL, F32_TOL, max_rel_err, np32
+from oracle import mla as ol
+from oracle import moe as om
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module")
+def dsk():
+    import ds_kernels
+    return ds_kernels
+
+
+@pytest.mark.parametrize("rows,H", [(4, 512), (64, 512), (1000, 512), (33, 2048), (8, 6),
+                                    (5, 4096), (3, 5000)])
+def test_rms_norm_bf16(dsk, rows, H):
+    g = torch.Generator().manual_seed(rows + H)
+    x = (torch.randn(rows, H, generator=g) * 0.5).to(torch.bfloat16)
+    w = torch.rand(H, generator=g) + 0.5
+    out = dsk.rms_norm(x.to(DEV), w.to(DEV), 1e-6)
+    assert out.dtype == torch.bfloat16 and out.shape == x.shape
+    ref = ol.rms_norm(np32(x), w.numpy(), 1e-6)
+    assert max_rel_err(np32(out), ref) <= BF16_TOL
+    np.testing.assert_allclose(np32(out), ref, rtol=2 ** -7, atol=1e-6)
+
+
+@pytest.mark.parametrize("rows,H", [(16, 512), (300, 2048), (7, 2050)])
+def test_rms_norm_f32(dsk, rows, H):
+    g = torch.Generator().manual_seed(rows)
+    x = torch.randn(rows, H, generator=g) * 3
+    w = torch.rand(H, generator=g) + 0.5
+    out = dsk.rms_norm(x.to(DEV), w.to(DEV), 1e-6)
+    ref = ol.rms_norm(x.numpy(), w.numpy(), 1e-6)
+    assert max_rel_err(np32(out), ref) <= F32_TOL
+    np.testing.assert_allclose(np32(out), ref, rtol=F32_TOL, atol=1e-6)
+
+
+def test_rms_norm_strided_latent_view(dsk):
+    """Normalise the 512-wide latent inside the 576-wide kv_a output in place."""
+    g = torch.Generator().manual_seed(3)
+    kva = torch.randn(2, 40, 576, generator=g).to(torch.bfloat16).to(DEV)
+    w = torch.ones(512, device=DEV)
+    out = dsk.rms_norm(kva[..., :512], w)
+    ref = ol.rms_norm(np32(kva[..., :512]), np.ones(512, np.float32))
+    assert max_rel_err(np32(out), ref) <= BF16_TOL
+
+
+def _rope_inputs(b, s, seed, strided=False):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(b, s, 16, 192, generator=g).to(torch.bfloat16)
+    kva = torch.randn(b, s, 576, generator=g).to(torch.bfloat16)
+    cos, sin = ol.yarn_cos_sin(s)
+    if strided:   # views straight out of the projections, as DeepSeekMLA makes them
+        q_pe = q.to(DEV).transpose(1, 2)[..., 128:]
+        k_pe = kva.to(DEV)[..., 512:].view(b, s, 1, 64).transpose(1, 2)
+    else:
+        q_pe = q.transpose(1, 2)[..., 128:].contiguous().to(DEV)
+        k_pe = kva[..., 512:].reshape(b, s, 1, 64).transpose(1, 2).contiguous().to(DEV)
+    cb = torch.from_numpy(cos).to(torch.bfloat16)[None, None].expand(b, 1, s, 64).contiguous()
+    sb = torch.from_numpy(sin).to(torch.bfloat16)[None, None].expand(b, 1, s, 64).contiguous()
+    return q_pe, k_pe, cb.to(DEV), sb.to(DEV)
+
+
+@pytest.mark.parametrize("b,s,strided", [(1, 16, False), (2, 64, False), (2, 64, True),
+                                         (1, 1, False), (8, 256, True)])
+def test_rope_matches_oracle(dsk, b, s, strided):
+    q_pe, k_pe, cos, sin = _rope_inputs(b, s, b * 1000 + s, strided)
+    q_rot, k_rot = dsk.rope(q_pe, k_pe, cos, sin)
+    assert q_rot.shape == (b, 16, s, 64) and k_rot.shape == (b, 1, s, 64)
+    c, sn = np32(cos), np32(sin)
+    rq = ol.rope(np32(q_pe), c, sn)
+    rk = ol.rope(np32(k_pe), c, sn)
+    assert max_rel_err(np32(q_rot), rq) <= BF16_TOL
+    assert max_rel_err(np32(k_rot), rk) <= BF16_TOL
+    np.testing.assert_allclose(np32(q_rot), rq, rtol=2 ** -7, atol=2e-3)
+
+
+@pytest.mark.parametrize("rows", [1, 64, 4096])
+def test_kv_upproj(dsk, rows):
+    g = torch.Generator().manual_seed(rows)
+    n = (torch.randn(rows, 512, generator=g) * 0.1).to(torch.bfloat16)
+    w = (torch.randn(4096, 512, generator=g) * 0.02).to(torch.bfloat16)
+    out = dsk.kv_upproj(n.to(DEV), w.to(DEV))
+    ref = om.grouped_linear(np32(n), np32(w)[None], np.array([0, rows], np.int32))
+    assert out.shape == (rows, 4096)
+    assert max_rel_err(np32(out), ref) <= BF16_TOL
+
+
+@pytest.mark.parametrize("M,K,N", [(8, 2048, 3072), (130, 2048, 576), (1000, 512, 4096),
+                                   (77, 128, 100)])
+def test_linear(dsk, M, K, N):
+    g = torch.Generator().manual_seed(M + N)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    out = dsk.linear(x.to(DEV), w.to(DEV))
+    ref = np32(x) @ np32(w).T
+    assert max_rel_err(np32(out), ref) <= BF16_TOL

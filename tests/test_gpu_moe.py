@@ -1,0 +1,273 @@
+"""GPU parity of the MoE ops and the fused layer against the numpy oracle.
+
+Bars: routing indices, counts, offsets, token_map, dispatched rows and weights
+bit-exact; bf16 outputs max|d|/max|ref| <= 2e-2 against the fp32 oracle on the
+same bf16-rounded inputs; fp32 routing weights <= 1e-5; every output bitwise
+identical run to run."""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from gpu_util import BF16_TOL, F32_TOL, max_rel_err, np32
+from oracle import moe as om
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+GOLD = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "kat.json")))
+
+
+@pytest.fixture(scope="module")
+def dsk():
+    import ds_kernels
+    return ds_kernels
+
+
+# ------------------------------------------------------------------ routing --
+@pytest.mark.parametrize("T,E,K", [(1, 64, 6), (32, 64, 6), (128, 64, 6), (4096, 64, 6),
+                                   (100, 16, 4), (65, 64, 1)])
+def test_routing_matches_oracle(dsk, T, E, K):
+    g = torch.Generator().manual_seed(T * 131 + E)
+    logits = torch.randn(T, E, generator=g)
+    idx, w, counts = dsk.moe_routing(logits.to(DEV), K)
+    ridx, rw, rcounts = om.route(logits.numpy(), K)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+    np.testing.assert_array_equal(counts.cpu().numpy(), rcounts)
+    assert max_rel_err(np32(w), rw) <= F32_TOL
+    np.testing.assert_allclose(np32(w), rw, rtol=F32_TOL, atol=1e-7)
+
+
+def test_routing_all_zero_kat(dsk):
+    kat = GOLD["routing_all_zero"]
+    logits = torch.zeros(kat["num_tokens"], kat["num_experts"], device=DEV)
+    idx, w, counts = dsk.moe_routing(logits, kat["top_k"])
+    assert all(r == kat["topk_indices_row"] for r in idx.cpu().tolist())
+    assert torch.all(w.cpu() == kat["topk_weight"])
+    assert counts.cpu().tolist() == kat["expert_counts"]
+
+
+def test_routing_ties_and_determinism(dsk):
+    logits = torch.randint(-2, 3, (300, 64)).float()   # heavy ties
+    a = dsk.moe_routing(logits.to(DEV), 6)
+    b = dsk.moe_routing(logits.to(DEV), 6)
+    ridx, _, _ = om.route(logits.numpy(), 6)
+    np.testing.assert_array_equal(a[0].cpu().numpy(), ridx)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+# --------------------------------------------------------------------- scan --
+@pytest.mark.parametrize("case", GOLD["scan"], ids=lambda c: c["name"])
+def test_scan_kat(dsk, case):
+    counts = torch.tensor(case["counts"], dtype=torch.int32, device=DEV)
+    assert dsk.moe_scan(counts).cpu().tolist() == case["offsets"]
+
+
+# ----------------------------------------------------------------- dispatch --
+@pytest.mark.parametrize("T", [1, 32, 128, 1000])
+def test_dispatch_matches_oracle(dsk, T):
+    g = torch.Generator().manual_seed(T)
+    logits = torch.randn(T, 64, generator=g)
+    x = torch.randn(T, 2048, generator=g).to(torch.bfloat16)
+    idx, w, counts = dsk.moe_routing(logits.to(DEV), 6)
+    off = dsk.moe_scan(counts)
+    disp, tm, dw = dsk.moe_dispatch(x.to(DEV), idx, w, off)
+    ridx, rw, rcounts = om.route(logits.numpy(), 6)
+    roff = om.scan(rcounts)
+    np.testing.assert_array_equal(off.cpu().numpy(), roff)
+    rdisp, rtm, rdw = om.dispatch(np32(x), ridx, np32(w), roff, 64)
+    np.testing.assert_array_equal(tm.cpu().numpy(), rtm)
+    np.testing.assert_array_equal(np32(dw), rdw)
+    np.testing.assert_array_equal(np32(disp), rdisp)
+    np.testing.assert_array_equal(np.bincount(rtm, minlength=T), np.full(T, 6))
+
+
+# ------------------------------------------------------------------ combine --
+def _combine_case(dsk, y, tm, dw, T):
+    out = dsk.moe_combine(y.to(DEV), tm.to(DEV), dw.to(DEV), T)
+    ref = om.combine(np32(y), tm.numpy(), dw.numpy(), T)
+    assert max_rel_err(np32(out), ref) <= BF16_TOL
+    # one rounding of the fp32 sum: within one bf16 ulp of the oracle everywhere
+    np.testing.assert_allclose(np32(out), ref, rtol=2 ** -7, atol=1e-6)
+    out2 = dsk.moe_combine(y.to(DEV), tm.to(DEV), dw.to(DEV), T)
+    assert torch.equal(out, out2)
+
+
+@pytest.mark.parametrize("T", [1, 7, 128])
+def test_combine_random_token_map(dsk, T):
+    g = torch.Generator().manual_seed(10 + T)
+    S = T * 6
+    y = torch.randn(S, 2048, generator=g).to(torch.bfloat16)
+    tm = torch.randint(0, T, (S,), generator=g, dtype=torch.int32)
+    dw = torch.rand(S, generator=g)
+    _combine_case(dsk, y, tm, dw, T)
+
+
+def test_combine_single_and_multi_slot(dsk):
+    g = torch.Generator().manual_seed(0)
+    T = 64
+    y = torch.randn(T, 2048, generator=g).to(torch.bfloat16)
+    _combine_case(dsk, y, torch.arange(T, dtype=torch.int32), torch.rand(T, generator=g), T)
+    y6 = torch.randn(T * 6, 2048, generator=g).to(torch.bfloat16)
+    tm6 = torch.repeat_interleave(torch.arange(T, dtype=torch.int32), 6)
+    _combine_case(dsk, y6, tm6, torch.rand(T * 6, generator=g), T)
+
+
+def test_combine_zero_weights_and_empty_tokens(dsk):
+    g = torch.Generator().manual_seed(1)
+    y = torch.randn(60, 2048, generator=g).to(torch.bfloat16)
+    tm = torch.randint(0, 5, (60,), generator=g, dtype=torch.int32)   # tokens 5..9 get nothing
+    out = dsk.moe_combine(y.to(DEV), tm.to(DEV), torch.zeros(60, device=DEV), 10)
+    assert torch.all(out == 0)
+    out = dsk.moe_combine(y.to(DEV), tm.to(DEV), torch.rand(60, device=DEV), 10)
+    assert torch.all(out[5:] == 0)
+
+
+# ------------------------------------------------------------------- swiglu --
+@pytest.mark.parametrize("rows", [0, 1, 8, 256])
+def test_swiglu(dsk, rows):
+    g = torch.Generator().manual_seed(rows)
+    x = (torch.rand(rows, 2816, generator=g) * 4 - 2).to(torch.bfloat16)
+    out = dsk.swiglu(x.to(DEV))
+    assert out.shape == (rows, 1408)
+    if rows:
+        ref = om.swiglu(np32(x))
+        assert max_rel_err(np32(out), ref) <= BF16_TOL
+        np.testing.assert_allclose(np32(out), ref, rtol=1e-2, atol=1e-2)
+
+
+# -------------------------------------------------------------------- GEMMs --
+def _round_robin_offsets(S, E):
+    counts = np.array([len(range(e, S, E)) for e in range(E)], np.int32)
+    return om.scan(counts)
+
+
+def _gemm_inputs(S, N, K, E, seed):
+    g = torch.Generator().manual_seed(seed)
+    a = (torch.rand(S, K, generator=g) * 2 - 1).to(torch.bfloat16)
+    w = (torch.rand(E, N, K, generator=g) * 0.1).to(torch.bfloat16)
+    return a, w
+
+
+@pytest.mark.parametrize("T", [1, 8, 32, 128])
+def test_gemm1_round_robin(dsk, T):
+    """test_moe_gemm1.py:58-119 shapes: 2048 -> 2816, round-robin offsets."""
+    S, E = T * 6, 64
+    a, w = _gemm_inputs(S, 2816, 2048, E, T)
+    off = _round_robin_offsets(S, E)
+    out = dsk.moe_gemm1(a.to(DEV), w.to(DEV), torch.from_numpy(off).to(DEV))
+    ref = om.grouped_linear(np32(a), np32(w), off)
+    assert out.shape == (S, 2816)
+    assert max_rel_err(np32(out), ref) <= BF16_TOL
+
+
+@pytest.mark.parametrize("T", [1, 32, 128])
+def test_gemm2_round_robin(dsk, T):
+    S, E = T * 6, 64
+    a, w = _gemm_inputs(S, 2048, 1408, E, 100 + T)
+    off = _round_robin_offsets(S, E)
+    out = dsk.moe_gemm2(a.to(DEV), w.to(DEV), torch.from_numpy(off).to(DEV))
+    ref = om.grouped_linear(np32(a), np32(w), off)
+    assert max_rel_err(np32(out), ref) <= BF16_TOL
+
+
+def test_gemm_skewed_groups_and_uncovered_rows(dsk):
+    """Empty experts, one big expert, partial tiles, rows past offsets[E] = 0."""
+    E = 8
+    counts = np.array([0, 300, 1, 0, 33, 129, 0, 64], np.int32)
+    off = om.scan(counts)
+    S = int(off[-1]) + 5
+    a, w = _gemm_inputs(S, 512, 256, E, 7)
+    out = dsk.moe_gemm2(a.to(DEV), w.to(DEV), torch.from_numpy(off).to(DEV))
+    ref = om.grouped_linear(np32(a), np32(w), off)
+    assert max_rel_err(np32(out), ref) <= BF16_TOL
+    assert torch.all(out[int(off[-1]):] == 0)
+
+
+def test_gemm_zero_slots(dsk):
+    out = dsk.moe_gemm1(torch.empty(0, 2048, dtype=torch.bfloat16, device=DEV),
+                        torch.zeros(64, 2816, 2048, dtype=torch.bfloat16, device=DEV),
+                        torch.zeros(65, dtype=torch.int32, device=DEV))
+    assert out.shape == (0, 2816)
+
+
+@pytest.mark.parametrize("T", [1, 64, 512])
+def test_gemm1_swiglu_fused(dsk, T):
+    S, E = T * 6, 64
+    a, w = _gemm_inputs(S, 2816, 2048, E, 200 + T)
+    off = _round_robin_offsets(S, E)
+    offd = torch.from_numpy(off).to(DEV)
+    out = dsk.moe_gemm1_swiglu(a.to(DEV), w.to(DEV), offd)
+    ref = om.swiglu(om.grouped_linear(np32(a), np32(w), off))
+    assert max_rel_err(np32(out), ref) <= BF16_TOL
+    unfused = dsk.swiglu(dsk.moe_gemm1(a.to(DEV), w.to(DEV), offd))
+    assert max_rel_err(np32(unfused), ref) <= BF16_TOL
+
+
+# ------------------------------------------------------------- fused layer --
+def _oracle_layer(Wn, x_bf, logits, K, shared=True):
+    return om.moe_layer(np32(x_bf), None, Wn["gates"], Wn["ups"], Wn["downs"], K,
+                        shared=Wn["shared"] if shared else None, logits=logits)
+
+
+@pytest.fixture(scope="module")
+def full_layer(dsk):
+    """Layer weights on the GPU (bf16, packed) and their bf16-rounded fp32
+    numpy copies for the oracle."""
+    from ds_kernels import synthetic as syn
+    W = syn.moe_weights()
+    w1, w2, nsh = dsk.pack_tensors(W.gates, W.ups, W.downs, device=torch.device(DEV),
+                                   shared=W.shared)
+    wb = lambda t: t.to(torch.bfloat16).float().numpy()  # noqa: E731
+    Wn = {"gates": wb(W.gates), "ups": wb(W.ups), "downs": wb(W.downs),
+          "shared": tuple(wb(t) for t in W.shared)}
+    return W, w1, w2, nsh, Wn
+
+
+@pytest.mark.parametrize("T,bias", [(64, False), (4096, False), (1, True), (4, True),
+                                    (16, True), (64, True)])
+def test_fused_layer_matches_oracle(dsk, full_layer, T, bias):
+    """Configs 0/1 (near-uniform routing) and 2 (Zipf-biased router), bf16."""
+    from ds_kernels import synthetic as syn
+    W, w1, w2, nsh, Wn = full_layer
+    x = syn.tokens(T).to(torch.bfloat16)
+    xd = x.to(DEV)
+    logits = F.linear(xd.float(), W.wg.to(torch.bfloat16).float().to(DEV))
+    if bias:
+        logits = logits + syn.zipf_router_bias().to(DEV)
+    logits = logits.contiguous()
+    out, (idx, w, off) = dsk.moe_fused_forward_logits(logits, xd, w1, w2, 6, nsh, 64,
+                                                      return_routing=True)
+    lg = logits.cpu().numpy()
+    ridx, rw, rcounts = om.route(lg, 6)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+    np.testing.assert_array_equal(off.cpu().numpy(), om.scan(rcounts))
+    np.testing.assert_allclose(np32(w), rw, rtol=F32_TOL, atol=1e-7)
+    ref = _oracle_layer(Wn, x, lg, 6)
+    err = max_rel_err(np32(out), ref)
+    assert err <= BF16_TOL, err
+    out2 = dsk.moe_fused_forward_logits(logits, xd, w1, w2, 6, nsh, 64)
+    assert torch.equal(out, out2)
+
+
+def test_op_pipeline_matches_fused(dsk, full_layer):
+    """Reference call sequence (routing->scan->dispatch->gemm1->swiglu->gemm2->combine),
+    routed experts only, vs the oracle without shared experts."""
+    from ds_kernels import synthetic as syn
+    W, w1, w2, nsh, Wn = full_layer
+    T = 256
+    x = syn.tokens(T).to(torch.bfloat16)
+    xd = x.to(DEV)
+    wg = W.wg.to(DEV)
+    packed_w1 = w1[:64].contiguous()
+    packed_w2 = w2[:64].contiguous()
+    out = dsk.route_dispatch_combine(xd, wg, packed_w1, packed_w2, 6)
+    out_f = dsk.route_dispatch_combine(xd, wg, packed_w1, packed_w2, 6, fuse_swiglu=True)
+    fused = dsk.fused_moe_forward(xd, wg, None, 6, packed_w1, packed_w2)
+    lg = F.linear(xd.float(), wg.float()).cpu().numpy()
+    ref = _oracle_layer(Wn, x, lg, 6, shared=False)
+    for o in (out, out_f, fused):
+        assert max_rel_err(np32(o), ref) <= BF16_TOL

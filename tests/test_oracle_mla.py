@@ -1,0 +1,90 @@
+"""Pins the numpy MLA oracle (CPU only): library routines, closed forms of the
+YaRN bands, complex-number RoPE, and torch SDPA for the attention core."""
+import math
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from oracle import mla as ol
+
+
+def test_rms_norm_matches_torch():
+    x = np.random.default_rng(0).standard_normal((33, 512)).astype(np.float32) * 3
+    w = np.random.default_rng(1).uniform(0.5, 1.5, 512).astype(np.float32)
+    ref = F.rms_norm(torch.from_numpy(x), (512,), torch.from_numpy(w), eps=1e-6).numpy()
+    np.testing.assert_allclose(ol.rms_norm(x, w, 1e-6), ref, rtol=1e-5, atol=1e-6)
+
+
+def test_rms_norm_bf16_rounding_point():
+    x = np.random.default_rng(2).standard_normal((4, 64)).astype(np.float32)
+    w = np.full(64, 3.0, np.float32)
+    xt = torch.from_numpy(x)
+    xh = (xt * torch.rsqrt(xt.pow(2).mean(-1, keepdim=True) + 1e-6)).to(torch.bfloat16).float()
+    np.testing.assert_allclose(ol.rms_norm(x, w, 1e-6, round_bf16=True), 3.0 * xh.numpy(),
+                               rtol=1e-6, atol=1e-6)
+
+
+def test_yarn_correction_range_and_bands():
+    lo, hi = ol.yarn_find_correction_range(32, 1, 64, 10000, 4096)
+    assert (lo, hi) == (10, 23)
+    inv = ol.yarn_inv_freq(64, 10000.0, 40.0, 4096, 32, 1)
+    i = np.arange(32)
+    extra = 1.0 / 10000.0 ** (2 * i / 64)
+    # below the ramp: pure extrapolation; above it: interpolation by the factor
+    np.testing.assert_allclose(inv[:lo + 1], extra[:lo + 1], rtol=1e-6)
+    np.testing.assert_allclose(inv[hi:], extra[hi:] / 40.0, rtol=1e-6)
+    # inside the ramp the value lies strictly between the two
+    mid = slice(lo + 1, hi)
+    assert np.all(inv[mid] < extra[mid]) and np.all(inv[mid] > extra[mid] / 40.0)
+    assert ol.yarn_get_mscale(40, 0.707) / ol.yarn_get_mscale(40, 0.707) == 1.0
+
+
+def test_yarn_tables_shape_and_symmetry():
+    cos, sin = ol.yarn_cos_sin(128)
+    assert cos.shape == (128, 64)
+    np.testing.assert_array_equal(cos[:, :32], cos[:, 32:])
+    np.testing.assert_array_equal(sin[:, :32], sin[:, 32:])
+    np.testing.assert_allclose(cos[0], 1.0)
+    np.testing.assert_allclose(sin[0], 0.0)
+
+
+def test_rope_is_complex_rotation():
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((2, 3, 5, 64)).astype(np.float32)
+    theta = rng.uniform(-3, 3, (5, 32)).astype(np.float32)
+    cos = np.concatenate([np.cos(theta)] * 2, -1)
+    sin = np.concatenate([np.sin(theta)] * 2, -1)
+    out = ol.rope(x, cos, sin)
+    z = (x[..., 0::2] + 1j * x[..., 1::2]) * np.exp(1j * theta)
+    np.testing.assert_allclose(out[..., :32], z.real, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(out[..., 32:], z.imag, rtol=1e-5, atol=1e-5)
+
+
+def test_attention_matches_torch_sdpa():
+    rng = np.random.default_rng(4)
+    q, k, v = (rng.standard_normal((2, 3, 17, 24)).astype(np.float32) for _ in range(3))
+    out = ol.attention(q, k, v, 0.3)
+    ref = F.scaled_dot_product_attention(torch.from_numpy(q), torch.from_numpy(k),
+                                         torch.from_numpy(v), is_causal=True, scale=0.3)
+    np.testing.assert_allclose(out, ref.numpy(), rtol=1e-5, atol=1e-5)
+
+
+def test_mla_forward_causal_and_shapes():
+    """Small-shape MLA: causality (reference test_reference_mla.py:71-96)."""
+    rng = np.random.default_rng(5)
+    H, nh, nope, r, vd, kl = 64, 2, 16, 8, 16, 32
+    p = dict(w_q=rng.standard_normal((nh * (nope + r), H)) * 0.1,
+             w_kva=rng.standard_normal((kl + r, H)) * 0.1, w_kva_norm=np.ones(kl),
+             w_kvb=rng.standard_normal((nh * (nope + vd), kl)) * 0.1,
+             w_o=rng.standard_normal((H, nh * vd)) * 0.1)
+    p = {k: v.astype(np.float32) for k, v in p.items()}
+    x = rng.standard_normal((1, 9, H)).astype(np.float32)
+    kw = dict(n_heads=nh, nope=nope, rope_dim=r, v_dim=vd, kv_lora=kl)
+    y = ol.mla_forward(x, **p, **kw)
+    assert y.shape == (1, 9, H)
+    x2 = x.copy()
+    x2[:, 5:] += 1.0
+    y2 = ol.mla_forward(x2, **p, **kw)
+    np.testing.assert_allclose(y[:, :5], y2[:, :5], rtol=1e-5, atol=1e-5)
+    assert not np.allclose(y[:, 5:], y2[:, 5:])
