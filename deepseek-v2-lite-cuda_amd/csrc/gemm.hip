@@ -15,13 +15,17 @@
 // M-tiles that share a weight tile run at the same time on the same XCD, so the
 // weight tile is fetched from HBM once and re-read from that XCD's L2.
 //
-// Tile: BM tokens x BN weight rows x 64 (K) per stage, two LDS stages
-// (global->register prefetch of stage k+1 overlaps the MFMAs of stage k). LDS
-// rows are 128 B with a 16-byte-chunk XOR swizzle (chunk ^ (row & 7)), so both
-// the coalesced row stores and the MFMA fragment reads (32 rows x one chunk)
-// are bank-conflict free. The weight fragment is MFMA operand A and the token
-// fragment operand B, so each lane ends up owning 4 consecutive output columns
-// of one token row (8-byte stores).
+// Data movement: BM tokens x BN weight rows x 64 (K) per stage, in a ring of
+// kStages LDS stages filled by direct global->LDS DMA (global_load_lds_dwordx4,
+// no register staging): while the MFMAs consume stage k, the loads of stages
+// k+1 .. k+kStages-1 are in flight. One workgroup barrier per K step.
+// LDS rows are 128 B with a 16-byte-chunk XOR swizzle
+// chunk ^ (row & 7) ^ ((row >> 3) & 1): with 64 banks of 4 B, 16 lanes of a
+// ds_read_b128 (16 rows, one logical chunk) then hit 16 distinct bank quads.
+// A DMA instruction writes 1 KB = 8 rows, lane l landing at row l/8, chunk
+// l%8, so lane l fetches the logical chunk that the swizzle puts there.
+// The weight fragment is MFMA operand A and the token fragment operand B, so
+// each lane owns 4 consecutive output columns of one token row (8-byte stores).
 //
 // SWIGLU mode fuses the SwiGLU activation into the epilogue: each wave's
 // weight rows are half gate rows (j) and half the matching up rows (I + j), so
@@ -31,6 +35,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <mutex>
+#include <type_traits>
 
 namespace dsk {
 
@@ -38,9 +43,85 @@ constexpr int kMaxGroups = 128;
 constexpr int kGemmThreads = 256;
 constexpr int kBK = 64;
 
+// Tile configuration (build-time; tuned on MI355X).
+#ifndef DSK_GEMM_BM
+#define DSK_GEMM_BM 128
+#endif
+#ifndef DSK_GEMM_BN
+#define DSK_GEMM_BN 256
+#endif
+#ifndef DSK_GEMM_WAVES_M
+#define DSK_GEMM_WAVES_M 1
+#endif
+#ifndef DSK_GEMM_STAGES
+#define DSK_GEMM_STAGES 3
+#endif
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void global_void_t;
+
 __device__ __forceinline__ float silu_f(float x) { return x / (1.f + __expf(-x)); }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool SWIGLU>
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+
+// 16-byte slot of (row, logical chunk) in a tile of 128-byte LDS rows.
+__device__ __forceinline__ int lds_swz(int row, int chunk) {
+  return row * 8 + (chunk ^ (row & 7) ^ ((row >> 3) & 1));
+}
+
+// Wait until at most min(ahead, MAXA) * NL vector-memory ops are pending.
+template <int MAXA, int NL>
+__device__ __forceinline__ void wait_stage_landed(int ahead) {
+  if constexpr (MAXA <= 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (ahead >= MAXA) wait_vmcnt<MAXA * NL>();
+    else wait_stage_landed<MAXA - 1, NL>(ahead);
+  }
+}
+
+// Workgroup barrier without the release/acquire fences of __syncthreads():
+// those would wait for every in-flight DMA (vmcnt(0)) and drain the ring. The
+// DMA completion this barrier publishes is waited for explicitly (wait_vmcnt)
+// by every wave before it arrives; the "memory" clobber keeps the compiler
+// from moving LDS accesses across the barrier.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// Scheduling groups for one K step: NMFMA MFMAs with the NREAD fragment reads
+// of the next step placed two after each of the first MFMAs (masks: 0x008 MFMA,
+// 0x100 LDS read).
+template <int NREAD, int NMFMA, int R = 0>
+__device__ __forceinline__ void sched_mfma_reads() {
+  constexpr int PAIRS = (NREAD + 1) / 2 < NMFMA ? (NREAD + 1) / 2 : NMFMA;
+  if constexpr (R < PAIRS) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, (2 * R + 2 <= NREAD) ? 2 : 1, 0);
+    sched_mfma_reads<NREAD, NMFMA, R + 1>();
+  } else {
+    if constexpr (NMFMA > PAIRS) __builtin_amdgcn_sched_group_barrier(0x008, NMFMA - PAIRS, 0);
+    if constexpr (NREAD > 2 * PAIRS)
+      __builtin_amdgcn_sched_group_barrier(0x100, NREAD - 2 * PAIRS, 0);
+  }
+}
+
+// Calls f(std::integral_constant<int, min(v, N)>) for a runtime v in [0, N].
+template <int N, class F>
+__device__ __forceinline__ void dispatch_count(int v, F&& f) {
+  if constexpr (N == 0) {
+    f(std::integral_constant<int, 0>{});
+  } else {
+    if (v >= N) f(std::integral_constant<int, N>{});
+    else dispatch_count<N - 1>(v, f);
+  }
+}
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, bool SWIGLU>
 struct GemmCfg {
   static_assert(WAVES_M * WAVES_N == 4, "4 waves per workgroup");
   static constexpr int WM = BM / WAVES_M;
@@ -50,21 +131,26 @@ struct GemmCfg {
   static_assert(TM >= 1 && TN >= 1, "wave tile must hold at least one 32x32 block");
   static_assert(!SWIGLU || (TN % 2 == 0), "SwiGLU needs matching gate/up blocks");
   static constexpr int OUT_N = SWIGLU ? BN / 2 : BN;
-  static constexpr int A_LOADS = BM * (kBK / 8) / kGemmThreads;  // 16-byte chunks per thread
-  static constexpr int B_LOADS = BN * (kBK / 8) / kGemmThreads;
-  static_assert(A_LOADS >= 1 && B_LOADS >= 1, "tile too small");
-  static constexpr int STAGE_ELEMS = (BM + BN) * kBK;
-  static constexpr int LDS_BYTES = 2 * STAGE_ELEMS * 2;
+  // DMA instructions per wave per stage: each moves 8 rows x 128 B
+  static constexpr int A_INSTS = BM / 32;
+  static constexpr int B_INSTS = BN / 32;
+  static_assert(BM % 32 == 0 && BN % 32 == 0, "tile rows must be multiples of 32");
+  static constexpr int A_BYTES = BM * kBK * 2;
+  static constexpr int STAGE_BYTES = (BM + BN) * kBK * 2;
+  static constexpr int LDS_BYTES = STAGES * STAGE_BYTES;
+  static_assert(LDS_BYTES <= 150 * 1024, "LDS budget");
 };
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool SWIGLU>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, bool SWIGLU>
 __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs p) {
-  using Cfg = GemmCfg<BM, BN, WAVES_M, WAVES_N, SWIGLU>;
+  using Cfg = GemmCfg<BM, BN, WAVES_M, WAVES_N, STAGES, SWIGLU>;
+  constexpr int kStages = STAGES;
   constexpr int WM = Cfg::WM, WN = Cfg::WN, TM = Cfg::TM, TN = Cfg::TN;
   constexpr int OUT_N = Cfg::OUT_N;
-  constexpr int A_LOADS = Cfg::A_LOADS, B_LOADS = Cfg::B_LOADS;
+  constexpr int A_INSTS = Cfg::A_INSTS, B_INSTS = Cfg::B_INSTS;
+  constexpr int NL = A_INSTS + B_INSTS;  // DMA instructions per thread per stage
 
-  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+  extern __shared__ __attribute__((aligned(1024))) uint16_t lds[];
   __shared__ int s_inc[kMaxGroups];
   __shared__ int s_mb[kMaxGroups];
   __shared__ int s_me[kMaxGroups];
@@ -107,14 +193,13 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
   const int w_beg = xcd * share;
   const int w_end = min(w_beg + share, total);
 
-  const int ld_chunk = tid & 7;     // 16-byte chunk of a 128-byte LDS row
-  const int ld_row = tid >> 3;      // 0..31 (+32*i)
-  const int st_off = ld_row * 8 + (ld_chunk ^ (ld_row & 7));  // u32x4 units, +256*i
-  u32x4_t* lds4 = reinterpret_cast<u32x4_t*>(lds);
-  constexpr int STAGE4 = Cfg::STAGE_ELEMS / 8;
-  constexpr int A4 = BM * kBK / 8;
+  // DMA lane mapping: row l/8 of an 8-row group g = wave + 4i (so g & 1 is
+  // wave & 1), logical chunk = physical chunk ^ swizzle(row)
+  const int dma_row = lane >> 3;
+  const int dma_chunk = (lane & 7) ^ dma_row ^ (wave & 1);
+  const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
+  const u32x4_t* lds4 = reinterpret_cast<const u32x4_t*>(lds);
   const int nk = p.K / kBK;
-  const u32x4_t zero4 = {0u, 0u, 0u, 0u};
 
   for (int W = w_beg + q; W < w_end; W += per_xcd) {
     int lo = 0, hi = G - 1;
@@ -132,39 +217,53 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
     const int n0 = nt * OUT_N;
     const uint16_t* Bg = p.B + (int64_t)g * p.b_group_stride;
 
-    // ---- per-thread global source rows
-    const uint16_t* a_src[A_LOADS];
-    bool a_ok[A_LOADS];
+    // ---- per-lane DMA source rows (out-of-range rows read a valid row; their
+    // results land in output rows/columns that are never stored)
+    const uint16_t* a_src[A_INSTS];
 #pragma unroll
-    for (int i = 0; i < A_LOADS; ++i) {
-      const int m = m0 + ld_row + 32 * i;
-      bool ok = m < me;
-      int row = m;
-      if (ok && p.a_rows != nullptr) {
-        row = p.a_rows[m];
-        ok = row >= 0 && row < p.a_rows_limit;
+    for (int i = 0; i < A_INSTS; ++i) {
+      const int m = m0 + 8 * (wave + 4 * i) + dma_row;
+      const int mm = m < me ? m : m0;
+      int row = mm;
+      if (p.a_rows != nullptr) {
+        row = p.a_rows[mm];
+        row = (row >= 0 && row < p.a_rows_limit) ? row : 0;
       }
-      a_ok[i] = ok;
-      a_src[i] = p.A + (ok ? (int64_t)row * p.lda : 0) + ld_chunk * 8;
+      a_src[i] = p.A + (int64_t)row * p.lda + dma_chunk * 8;
     }
-    const uint16_t* b_src[B_LOADS];
-    bool b_ok[B_LOADS];
+    const uint16_t* b_src[B_INSTS];
 #pragma unroll
-    for (int i = 0; i < B_LOADS; ++i) {
-      const int r = ld_row + 32 * i;
+    for (int i = 0; i < B_INSTS; ++i) {
+      const int r = 8 * (wave + 4 * i) + dma_row;
       int brow, col;
       if constexpr (SWIGLU) {
         const int wn = r / WN, w = r % WN;
         constexpr int half = WN / 2;
-        col = n0 + wn * half + (w % half);
+        col = min(n0 + wn * half + (w % half), p.N - 1);
         brow = (w < half) ? col : p.up_row_offset + col;
       } else {
-        col = n0 + r;
+        col = min(n0 + r, p.N - 1);
         brow = col;
       }
-      b_ok[i] = col < p.N;
-      b_src[i] = Bg + (b_ok[i] ? (int64_t)brow * p.ldb : 0) + ld_chunk * 8;
+      b_src[i] = Bg + (int64_t)brow * p.ldb + dma_chunk * 8;
     }
+
+    auto issue = [&](int stage, int kt) {
+      const int koff = kt * kBK;
+      const uint32_t sbase = lds_base + stage * Cfg::STAGE_BYTES;
+#pragma unroll
+      for (int i = 0; i < A_INSTS; ++i) {
+        const uint32_t dst = sbase + (wave + 4 * i) * 1024;
+        __builtin_amdgcn_global_load_lds((global_void_t*)(a_src[i] + koff),
+                                         (lds_void_t*)(uintptr_t)dst, 16, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < B_INSTS; ++i) {
+        const uint32_t dst = sbase + Cfg::A_BYTES + (wave + 4 * i) * 1024;
+        __builtin_amdgcn_global_load_lds((global_void_t*)(b_src[i] + koff),
+                                         (lds_void_t*)(uintptr_t)dst, 16, 0, 0);
+      }
+    };
 
     int tm_active = (me - (m0 + wave_m * WM) + 31) / 32;
     tm_active = max(0, min(TM, tm_active));
@@ -177,66 +276,73 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.f;
 
-    u32x4_t ra[A_LOADS], rb[B_LOADS];
+    // prologue: stages 0 .. kStages-2 in flight
 #pragma unroll
-    for (int i = 0; i < A_LOADS; ++i)
-      ra[i] = a_ok[i] ? *reinterpret_cast<const u32x4_t*>(a_src[i]) : zero4;
-#pragma unroll
-    for (int i = 0; i < B_LOADS; ++i)
-      rb[i] = b_ok[i] ? *reinterpret_cast<const u32x4_t*>(b_src[i]) : zero4;
-#pragma unroll
-    for (int i = 0; i < A_LOADS; ++i) lds4[st_off + 256 * i] = ra[i];
-#pragma unroll
-    for (int i = 0; i < B_LOADS; ++i) lds4[A4 + st_off + 256 * i] = rb[i];
-    __syncthreads();
+    for (int s = 0; s < kStages - 1; ++s)
+      if (s < nk) issue(s, s);
 
-    for (int kt = 0; kt < nk; ++kt) {
-      const bool more = kt + 1 < nk;
-      if (more) {
-        const int koff = (kt + 1) * kBK;
+    // K loop, specialised on the number of active 32-row blocks of this wave
+    // (TMA) so the common full-tile case has no control flow around the MFMAs.
+    auto mainloop = [&](auto tma_c) {
+      constexpr int TMA = decltype(tma_c)::value;
+      for (int kt = 0; kt < nk; ++kt) {
+        // stage kt has landed when at most the loads of the stages issued after
+        // it (min(kStages - 2, nk - 1 - kt) of them) are pending
+        wait_stage_landed<kStages - 2, NL>(nk - 1 - kt);
+        lds_barrier();
+        if (kt + kStages - 1 < nk) issue((kt + kStages - 1) % kStages, kt + kStages - 1);
+        if constexpr (TMA > 0) {
+          const int stage = kt % kStages;
+          const u32x4_t* As = lds4 + stage * (Cfg::STAGE_BYTES / 16);
+          const u32x4_t* Bs = As + Cfg::A_BYTES / 16;
+          // fragments of K-step kk are read into register set kk&1 while the
+          // MFMAs of step kk-1 run from the other set
+          bf16x8_t fb[2][TN], fa[2][TMA];
+          auto read_frags = [&](int set, int kk) {
+            const int ch = 2 * kk + (lane >> 5);
 #pragma unroll
-        for (int i = 0; i < A_LOADS; ++i)
-          ra[i] = a_ok[i] ? *reinterpret_cast<const u32x4_t*>(a_src[i] + koff) : zero4;
+            for (int j = 0; j < TN; ++j) {
+              const int rr = wave_n * WN + 32 * j + (lane & 31);
+              fb[set][j] = __builtin_bit_cast(bf16x8_t, Bs[lds_swz(rr, ch)]);
+            }
 #pragma unroll
-        for (int i = 0; i < B_LOADS; ++i)
-          rb[i] = b_ok[i] ? *reinterpret_cast<const u32x4_t*>(b_src[i] + koff) : zero4;
-      }
-      const u32x4_t* As = lds4 + (kt & 1) * STAGE4;
-      const u32x4_t* Bs = As + A4;
+            for (int i = 0; i < TMA; ++i) {
+              const int rr = wave_m * WM + 32 * i + (lane & 31);
+              fa[set][i] = __builtin_bit_cast(bf16x8_t, As[lds_swz(rr, ch)]);
+            }
+          };
+          constexpr int KSTEPS = kBK / 16;
+          constexpr int NREAD = TN + TMA;   // ds_read_b128 per K-step
+          constexpr int NMFMA = TN * TMA;   // MFMAs per K-step
+          read_frags(0, 0);
 #pragma unroll
-      for (int kk = 0; kk < kBK / 16; ++kk) {
-        const int ch = 2 * kk + (lane >> 5);
-        bf16x8_t bfr[TN], afr[TM];
+          for (int kk = 0; kk < KSTEPS; ++kk) {
+            if (kk + 1 < KSTEPS) read_frags((kk + 1) & 1, kk + 1);
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          const int rr = wave_n * WN + 32 * j + (lane & 31);
-          bfr[j] = __builtin_bit_cast(bf16x8_t, Bs[rr * 8 + (ch ^ (rr & 7))]);
-        }
+            for (int i = 0; i < TMA; ++i)
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-          if (i < tm_active) {
-            const int rr = wave_m * WM + 32 * i + (lane & 31);
-            afr[i] = __builtin_bit_cast(bf16x8_t, As[rr * 8 + (ch ^ (rr & 7))]);
+              for (int j = 0; j < TN; ++j)
+                acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[kk & 1][j], fa[kk & 1][i],
+                                                                    acc[j][i], 0, 0, 0);
+          }
+          // schedule: step-0 reads, then each step's MFMAs with the next step's
+          // reads front-loaded (two reads after each of the first MFMAs), so the
+          // reads have most of the step's MFMAs to land
+          __builtin_amdgcn_sched_group_barrier(0x100, NREAD, 0);
+#pragma unroll
+          for (int kk = 0; kk < KSTEPS; ++kk) {
+            if (kk + 1 < KSTEPS) {
+              sched_mfma_reads<NREAD, NMFMA>();
+            } else {
+              __builtin_amdgcn_sched_group_barrier(0x008, NMFMA, 0);
+            }
           }
         }
-#pragma unroll
-        for (int i = 0; i < TM; ++i) {
-          if (i < tm_active) {
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
-              acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], afr[i], acc[j][i], 0, 0, 0);
-          }
-        }
       }
-      if (more) {
-        u32x4_t* Ad = lds4 + ((kt + 1) & 1) * STAGE4;
-#pragma unroll
-        for (int i = 0; i < A_LOADS; ++i) Ad[st_off + 256 * i] = ra[i];
-#pragma unroll
-        for (int i = 0; i < B_LOADS; ++i) Ad[A4 + st_off + 256 * i] = rb[i];
-      }
-      __syncthreads();
-    }
+    };
+    dispatch_count<TM>(tm_active, mainloop);
+    // all waves are done reading the ring before the next tile's prologue DMA
+    __syncthreads();
 
     // ---- epilogue: lane owns token row m = ... + (lane & 31) and 4 consecutive
     // output columns per 4-register group
@@ -305,10 +411,10 @@ static int num_cus() {
   return cached[dev];
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool SWIGLU>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, bool SWIGLU>
 static int launch_grouped_gemm(const GemmArgs& a, hipStream_t st) {
-  using Cfg = GemmCfg<BM, BN, WAVES_M, WAVES_N, SWIGLU>;
-  auto kern = grouped_gemm_kernel<BM, BN, WAVES_M, WAVES_N, SWIGLU>;
+  using Cfg = GemmCfg<BM, BN, WAVES_M, WAVES_N, STAGES, SWIGLU>;
+  auto kern = grouped_gemm_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, SWIGLU>;
   static std::once_flag once;
   std::call_once(once, [&] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -352,8 +458,10 @@ static int validate_gemm(const GemmArgs& a, const char* who) {
 // the end of its group.
 int run_gemm(const GemmArgs& a, bool swiglu, hipStream_t st) {
   if (a.M == 0) return DSK_OK;
-  if (swiglu) return launch_grouped_gemm<128, 256, 1, 4, true>(a, st);
-  return launch_grouped_gemm<128, 256, 1, 4, false>(a, st);
+  constexpr int BM = DSK_GEMM_BM, BN = DSK_GEMM_BN, WAVES_M = DSK_GEMM_WAVES_M;
+  constexpr int STAGES = DSK_GEMM_STAGES;
+  if (swiglu) return launch_grouped_gemm<BM, BN, WAVES_M, 4 / WAVES_M, STAGES, true>(a, st);
+  return launch_grouped_gemm<BM, BN, WAVES_M, 4 / WAVES_M, STAGES, false>(a, st);
 }
 
 int zero_uncovered_rows(uint16_t* C, int64_t ldc, int M, int N, const int32_t* offsets,

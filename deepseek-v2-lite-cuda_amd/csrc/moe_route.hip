@@ -20,9 +20,11 @@
 
 namespace dsk {
 
-constexpr int kChunk = 64;          // tokens per routing workgroup (= mask width)
-constexpr int kRouteThreads = 256;  // 4 waves, 16 tokens each
-constexpr int kTokPerWave = kChunk / (kRouteThreads / kWave);
+constexpr int kChunk = 64;            // tokens per routing workgroup (= mask width)
+constexpr int kRouteThreads = 1024;   // 16 waves, 4 tokens each
+constexpr int kRouteWaves = kRouteThreads / kWave;
+constexpr int kTokPerWave = kChunk / kRouteWaves;
+constexpr int kRankThreads = 256;
 
 // ------------------------------------------------------------------ route --
 // One wave per token, one expert logit per lane. Writes topk idx / weights,
@@ -46,14 +48,22 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(
   __syncthreads();
 
   const int t0 = blockIdx.x * kChunk;
+  // all of this wave's logit loads are issued before any reduction, so their
+  // latency is paid once rather than once per token
+  float xs[kTokPerWave];
+#pragma unroll
+  for (int i = 0; i < kTokPerWave; ++i) {
+    const int t = t0 + wave + kRouteWaves * i;
+    xs[i] = (t < T && lane < E) ? logits[(int64_t)t * ld + lane] : -INFINITY;
+  }
   int my_e[kTokPerWave];
 #pragma unroll
   for (int i = 0; i < kTokPerWave; ++i) {
     my_e[i] = -1;
-    const int tl = wave + 4 * i;
+    const int tl = wave + kRouteWaves * i;
     const int t = t0 + tl;
     if (t < T) {  // wave-uniform
-      const float x = lane < E ? logits[(int64_t)t * ld + lane] : -INFINITY;
+      const float x = xs[i];
       const float mx = wave_max(x);
       const float ex = lane < E ? expf(x - mx) : 0.f;
       const float sum = wave_sum(ex);
@@ -90,7 +100,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(
   int rank[kTokPerWave];
 #pragma unroll
   for (int i = 0; i < kTokPerWave; ++i) {
-    const int tl = wave + 4 * i;
+    const int tl = wave + kRouteWaves * i;
     rank[i] = my_e[i] >= 0 ? __popcll(s_mask[my_e[i]] & ((1ull << tl) - 1ull)) : -1;
     if (local_rank != nullptr && my_e[i] >= 0)
       local_rank[(int64_t)(t0 + tl) * K + lane] = rank[i];
@@ -115,7 +125,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(
 #pragma unroll
       for (int i = 0; i < kTokPerWave; ++i) {
         if (my_e[i] >= 0) {
-          const int t = t0 + wave + 4 * i;
+          const int t = t0 + wave + kRouteWaves * i;
           const int slot = s_off[my_e[i]] + rank[i];
           token_map[slot] = t;
           if (slot_of != nullptr) slot_of[(int64_t)t * K + lane] = slot;
@@ -132,7 +142,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(
 // Chunk histogram + in-chunk stable rank from a given topk_idx (the dispatch
 // op receives indices, not logits). Entries with an out-of-range expert, or a
 // repeat of an expert earlier in the same row, get rank -1 and are skipped.
-__global__ __launch_bounds__(kRouteThreads) void rank_kernel(
+__global__ __launch_bounds__(kRankThreads) void rank_kernel(
     const int32_t* __restrict__ idx, int T, int K, int E,
     int32_t* __restrict__ blk_hist, int32_t* __restrict__ local_rank) {
   __shared__ unsigned long long s_mask[64];
@@ -141,7 +151,7 @@ __global__ __launch_bounds__(kRouteThreads) void rank_kernel(
   __syncthreads();
   const int t0 = blockIdx.x * kChunk;
   const int npairs = kChunk * K;
-  for (int p = tid; p < npairs; p += kRouteThreads) {
+  for (int p = tid; p < npairs; p += kRankThreads) {
     const int tl = p / K, k = p - tl * K;
     const int t = t0 + tl;
     if (t >= T) continue;
@@ -152,7 +162,7 @@ __global__ __launch_bounds__(kRouteThreads) void rank_kernel(
   }
   __syncthreads();
   if (tid < E) blk_hist[(int64_t)blockIdx.x * E + tid] = __popcll(s_mask[tid]);
-  for (int p = tid; p < npairs; p += kRouteThreads) {
+  for (int p = tid; p < npairs; p += kRankThreads) {
     const int tl = p / K, k = p - tl * K;
     const int t = t0 + tl;
     if (t >= T) continue;
@@ -579,7 +589,7 @@ extern "C" int dsk_moe_dispatch(const dsk_bf16* x, int64_t ld_x, const int32_t* 
   int32_t* base = reinterpret_cast<int32_t*>(ws + nb);
   int32_t* rank = reinterpret_cast<int32_t*>(ws + 2 * nb);
   int32_t* slot_of = reinterpret_cast<int32_t*>(ws + 2 * nb + pairs);
-  hipLaunchKernelGGL(rank_kernel, dim3(nblk), dim3(kRouteThreads), 0, st, topk_idx,
+  hipLaunchKernelGGL(rank_kernel, dim3(nblk), dim3(kRankThreads), 0, st, topk_idx,
                      num_tokens, top_k, num_experts, hist, rank);
   int rc = check_launch("rank_kernel");
   if (rc) return rc;
