@@ -171,7 +171,62 @@ def cpu_baseline(W, syn, budget_s):
                       f"{n} calls in {el:.1f} s, BLAS threads={threads}, host cpus={os.cpu_count()}"}
 
 
+COPY_BYTES = 1 << 30  # calibration copy: 1 GiB read + 1 GiB written per launch
+
+
+def calibrate_copy(steps):
+    """Plain device copy of COPY_BYTES, the reference kernel for the HBM counters:
+    FETCH_SIZE / WRITE_SIZE of the GEMM are scaled by what the counters read here
+    against the known 1 GiB."""
+    import torch
+    src = torch.empty(COPY_BYTES // 2, dtype=torch.bfloat16, device="cuda:0").normal_()
+    dst = torch.empty_like(src)
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": COPY_BYTES, "launches": steps}), flush=True)
+
+
+def _pmc_per_dispatch(csv_path, kernel_substrs, counter):
+    import csv
+    vals = {}
+    with open(csv_path) as f:
+        for r in csv.DictReader(f):
+            if (all(k in r["Kernel_Name"] for k in kernel_substrs)
+                    and r["Counter_Name"].startswith(counter)):
+                vals[r["Dispatch_Id"]] = vals.get(r["Dispatch_Id"], 0.0) + float(
+                    r["Counter_Value"])
+    return sorted(vals.values())
+
+
+def summarize_traffic(gemm_fetch, gemm_write, copy_fetch, copy_write, out_path):
+    """HBM bytes per launch of the SwiGLU GEMM from rocprofv3 --pmc CSVs
+    (FETCH_SIZE and WRITE_SIZE passes over `bench.py --profile` and over
+    `bench.py --calibrate-copy`), each scaled by the copy's counter/byte ratio."""
+    kib = 1024.0
+    med = lambda v: v[len(v) // 2]  # noqa: E731
+    cf = _pmc_per_dispatch(copy_fetch, (), "FETCH_SIZE")
+    cw = _pmc_per_dispatch(copy_write, (), "WRITE_SIZE")
+    # the copy is the only large kernel in its run: take its biggest dispatch
+    f_scale = COPY_BYTES / (max(cf) * kib)
+    w_scale = COPY_BYTES / (max(cw) * kib)
+    swiglu_gather = ("grouped_gemm_kernel", "true, true>")  # SWIGLU, GATHER
+    gf = med(_pmc_per_dispatch(gemm_fetch, swiglu_gather, "FETCH_SIZE"))
+    gw = med(_pmc_per_dispatch(gemm_write, swiglu_gather, "WRITE_SIZE"))
+    res = {"kernel": "grouped_gemm_kernel SwiGLU+gather (gemm1), T=4096",
+           "fetch_kib_raw": gf, "write_kib_raw": gw,
+           "fetch_scale": f_scale, "write_scale": w_scale,
+           "hbm_read_bytes": gf * kib * f_scale, "hbm_write_bytes": gw * kib * w_scale,
+           "hbm_bytes_per_launch": gf * kib * f_scale + gw * kib * w_scale}
+    with open(out_path, "w") as f:
+        json.dump(res, f, indent=1)
+    print(json.dumps(res))
+
+
 def main():
+    if len(sys.argv) > 1 and sys.argv[1] == "--summarize-traffic":
+        summarize_traffic(*sys.argv[2:7])
+        return
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
@@ -181,7 +236,12 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--profile", action="store_true",
                     help="prefill steps only (no decode sweep, no CPU baseline)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run only the 1 GiB device copy used to scale the HBM counters")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        calibrate_copy(3)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
               "(multi-GPU sharding is design-only, see the sharding section of the docs)",

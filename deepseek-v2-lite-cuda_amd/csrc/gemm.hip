@@ -12,20 +12,35 @@
 // Scheduling: a persistent grid (one workgroup per CU). Output tiles are
 // enumerated group-major, then N-tile, then M-tile, and the enumeration is cut
 // into 8 contiguous ranges, one per XCD (workgroup i runs on XCD i % 8): the
-// M-tiles that share a weight tile run at the same time on the same XCD, so the
-// weight tile is fetched from HBM once and re-read from that XCD's L2.
+// M-tiles that share a weight tile run at about the same time on the same XCD,
+// so the weight tile is mostly re-read from that XCD's L2.
 //
-// Data movement: BM tokens x BN weight rows x 64 (K) per stage, in a ring of
-// kStages LDS stages filled by direct global->LDS DMA (global_load_lds_dwordx4,
-// no register staging): while the MFMAs consume stage k, the loads of stages
-// k+1 .. k+kStages-1 are in flight. One workgroup barrier per K step.
-// LDS rows are 128 B with a 16-byte-chunk XOR swizzle
-// chunk ^ (row & 7) ^ ((row >> 3) & 1): with 64 banks of 4 B, 16 lanes of a
-// ds_read_b128 (16 rows, one logical chunk) then hit 16 distinct bank quads.
-// A DMA instruction writes 1 KB = 8 rows, lane l landing at row l/8, chunk
-// l%8, so lane l fetches the logical chunk that the swizzle puts there.
+// Data movement: each workgroup runs one continuous stream of K stages over
+// all of its tiles. A stage (BM token rows + BN weight rows, BK deep) lands in
+// a ring of STAGES LDS buffers through direct global->LDS DMA
+// (global_load_lds_dwordx4, no register staging), issued STAGES-1 stages
+// ahead, so the next tile's first stage is in flight while the current one
+// finishes and writes its epilogue. One workgroup barrier per stage, placed
+// before the last K step: that step's MFMAs then overlap the next stage's
+// first fragment reads and the refill DMA of the buffer just released.
+//
+// The L2->CU path (~48 B/clk per CU measured, for DMA and vector loads alike)
+// and its latency, rather than the matrix cores, bound this kernel at small
+// tiles, so tiles are as large as the accumulators allow: 256 tokens x 256
+// weight rows (128 flops per byte moved), 8 waves of 128 x 64 (two per SIMD,
+// so one wave's MFMAs cover the other's waits), BK = 64 so every DMA row is a
+// whole 128-byte line, and a 2-deep ring (2 x 64 KB of the 160 KB LDS).
+//
+// LDS rows are BK*2 bytes with a 16-byte-chunk XOR swizzle chosen so the 16
+// lanes that the 64-bank LDS serves together (16 rows, one logical chunk of a
+// fragment read) hit 16 distinct bank quads. A DMA instruction writes 1 KB
+// (64 lanes x 16 B) = 1024 / (BK*2) rows; lane l lands at a fixed physical
+// slot, so it fetches the logical chunk the swizzle puts there.
 // The weight fragment is MFMA operand A and the token fragment operand B, so
 // each lane owns 4 consecutive output columns of one token row (8-byte stores).
+// Partial M tiles skip the MFMAs of 32-row blocks past the group end; the
+// variant (all blocks, half, none) is chosen once per tile so the K loop itself
+// has no data-dependent branches around the accumulators.
 //
 // SWIGLU mode fuses the SwiGLU activation into the epilogue: each wave's
 // weight rows are half gate rows (j) and half the matching up rows (I + j), so
@@ -40,39 +55,52 @@
 namespace dsk {
 
 constexpr int kMaxGroups = 128;
-constexpr int kGemmThreads = 256;
-constexpr int kBK = 64;
+constexpr int kTileChunk = 16;  // tiles dealt to one XCD at a time
+constexpr int kLdsPerCU = 160 * 1024;
 
 // Tile configuration (build-time; tuned on MI355X).
 #ifndef DSK_GEMM_BM
-#define DSK_GEMM_BM 128
+#define DSK_GEMM_BM 256
 #endif
 #ifndef DSK_GEMM_BN
 #define DSK_GEMM_BN 256
 #endif
 #ifndef DSK_GEMM_WAVES_M
-#define DSK_GEMM_WAVES_M 1
+#define DSK_GEMM_WAVES_M 2
+#endif
+#ifndef DSK_GEMM_WAVES_N
+#define DSK_GEMM_WAVES_N 4
+#endif
+#ifndef DSK_GEMM_BK
+#define DSK_GEMM_BK 64
 #endif
 #ifndef DSK_GEMM_STAGES
-#define DSK_GEMM_STAGES 3
+#define DSK_GEMM_STAGES 2
 #endif
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void global_void_t;
 
-__device__ __forceinline__ float silu_f(float x) { return x / (1.f + __expf(-x)); }
+// silu(x) = x / (1 + e^-x) with the hardware reciprocal (1 ulp), ample for a
+// result that is rounded to bf16.
+__device__ __forceinline__ float silu_f(float x) {
+  return x * __builtin_amdgcn_rcpf(1.f + __expf(-x));
+}
 
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
 // vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
+// Reads an accumulator register where it is used: the epilogue then moves
+// the accumulators to VGPRs a few at a time instead of all at once.
+__device__ __forceinline__ float acc_read(float a) {
+  float v;
+  asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
+  return v;
+}
+
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
-}
-
-// 16-byte slot of (row, logical chunk) in a tile of 128-byte LDS rows.
-__device__ __forceinline__ int lds_swz(int row, int chunk) {
-  return row * 8 + (chunk ^ (row & 7) ^ ((row >> 3) & 1));
 }
 
 // Wait until at most min(ahead, MAXA) * NL vector-memory ops are pending.
@@ -110,20 +138,24 @@ __device__ __forceinline__ void sched_mfma_reads() {
   }
 }
 
-// Calls f(std::integral_constant<int, min(v, N)>) for a runtime v in [0, N].
-template <int N, class F>
-__device__ __forceinline__ void dispatch_count(int v, F&& f) {
+// Calls f(std::integral_constant<int, n>) for the runtime value n in [0, N].
+template <int N, typename F>
+__device__ __forceinline__ void dispatch_active(int n, F&& f) {
   if constexpr (N == 0) {
     f(std::integral_constant<int, 0>{});
   } else {
-    if (v >= N) f(std::integral_constant<int, N>{});
-    else dispatch_count<N - 1>(v, f);
+    if (n >= N) f(std::integral_constant<int, N>{});
+    else dispatch_active<N - 1>(n, f);
   }
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, bool SWIGLU>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int BK, int STAGES, bool SWIGLU>
 struct GemmCfg {
-  static_assert(WAVES_M * WAVES_N == 4, "4 waves per workgroup");
+  static constexpr int NW = WAVES_M * WAVES_N;  // waves per workgroup
+  static_assert(NW == 4 || NW == 8, "4 or 8 waves per workgroup");
+  static constexpr int THREADS = 64 * NW;
+  static_assert(BK == 32 || BK == 64, "BK is 32 or 64");
+  static_assert(STAGES >= 2, "the stage stream needs at least 2 LDS buffers");
   static constexpr int WM = BM / WAVES_M;
   static constexpr int WN = BN / WAVES_N;
   static constexpr int TM = WM / 32;
@@ -131,24 +163,41 @@ struct GemmCfg {
   static_assert(TM >= 1 && TN >= 1, "wave tile must hold at least one 32x32 block");
   static_assert(!SWIGLU || (TN % 2 == 0), "SwiGLU needs matching gate/up blocks");
   static constexpr int OUT_N = SWIGLU ? BN / 2 : BN;
-  // DMA instructions per wave per stage: each moves 8 rows x 128 B
-  static constexpr int A_INSTS = BM / 32;
-  static constexpr int B_INSTS = BN / 32;
-  static_assert(BM % 32 == 0 && BN % 32 == 0, "tile rows must be multiples of 32");
-  static constexpr int A_BYTES = BM * kBK * 2;
-  static constexpr int STAGE_BYTES = (BM + BN) * kBK * 2;
-  static constexpr int LDS_BYTES = STAGES * STAGE_BYTES;
-  static_assert(LDS_BYTES <= 150 * 1024, "LDS budget");
+  static constexpr int CPR = BK / 8;        // 16-byte chunks per LDS row
+  static constexpr int RPI = 64 / CPR;      // rows per 1 KB DMA instruction
+  static constexpr int A_INSTS = BM / (NW * RPI);  // DMA instructions per wave per stage
+  static constexpr int B_INSTS = BN / (NW * RPI);
+  static_assert(A_INSTS * NW * RPI == BM && B_INSTS * NW * RPI == BN, "tile rows vs DMA rows");
+  static constexpr int KSTEPS = BK / 16;
+  static constexpr int A_BYTES = BM * BK * 2;
+  static constexpr int STAGE_BYTES = (BM + BN) * BK * 2;
+  static constexpr int RING_BYTES = STAGES * STAGE_BYTES;
+  // tiles per workgroup whose gathered A row indices fit in the LDS left over
+  // (4 KB kept for the group table and alignment)
+  static constexpr int ROW_TILES = (kLdsPerCU - RING_BYTES - 4096) / (BM * 4);
+  static_assert(ROW_TILES >= 1, "no LDS left for the row table");
+  static constexpr int LDS_BYTES = RING_BYTES + ROW_TILES * BM * 4;  // dynamic LDS
 };
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, bool SWIGLU>
-__global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs p) {
-  using Cfg = GemmCfg<BM, BN, WAVES_M, WAVES_N, STAGES, SWIGLU>;
+// 16-byte slot of (row, logical chunk) in a tile of CPR-chunk LDS rows.
+template <int CPR>
+__device__ __forceinline__ int lds_swz(int row, int chunk) {
+  if constexpr (CPR == 8) return row * 8 + (chunk ^ (row & 7) ^ ((row >> 3) & 1));
+  else return row * 4 + (chunk ^ ((row >> 2) & 3));
+}
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, int BK, int STAGES, bool SWIGLU,
+          bool GATHER>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void grouped_gemm_kernel(GemmArgs p) {
+  using Cfg = GemmCfg<BM, BN, WAVES_M, WAVES_N, BK, STAGES, SWIGLU>;
   constexpr int kStages = STAGES;
   constexpr int WM = Cfg::WM, WN = Cfg::WN, TM = Cfg::TM, TN = Cfg::TN;
   constexpr int OUT_N = Cfg::OUT_N;
+  constexpr int CPR = Cfg::CPR, RPI = Cfg::RPI;
   constexpr int A_INSTS = Cfg::A_INSTS, B_INSTS = Cfg::B_INSTS;
   constexpr int NL = A_INSTS + B_INSTS;  // DMA instructions per thread per stage
+  constexpr int KSTEPS = Cfg::KSTEPS;
+  constexpr int NW = Cfg::NW;
 
   extern __shared__ __attribute__((aligned(1024))) uint16_t lds[];
   __shared__ int s_inc[kMaxGroups];
@@ -157,13 +206,18 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // wave index as a uniform (scalar) value, so per-wave decisions are branches
+  // rather than exec-masked code
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wave_m = wave / WAVES_N;
   const int wave_n = wave % WAVES_N;
   const int G = p.offsets != nullptr ? p.G : 1;
   const int NT = (p.N + OUT_N - 1) / OUT_N;
 
-  // ---- group table: row ranges and inclusive prefix of tile counts
+  // ---- group table: row ranges and inclusive prefix of tile counts. A
+  // group of n rows is cut into mt = ceil(n / BM) M tiles of equal size (in
+  // 32-row blocks, +-1 block), so the M tiles that share a weight tile
+  // progress at the same rate and read it from L2 together.
   if (tid < kMaxGroups) {
     int cnt = 0;
     if (tid < G) {
@@ -183,203 +237,280 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
   __syncthreads();
   if (tid >= 64 && tid < kMaxGroups) s_inc[tid] += carry;
   __syncthreads();
-  const int total = s_inc[G - 1];
+  const int total_tiles = s_inc[G - 1];
 
-  // ---- XCD-aware persistent enumeration
+  // ---- XCD-aware persistent enumeration. Tiles (group-major, then N tile,
+  // then M tile) are dealt to the 8 XCDs in chunks of kChunk consecutive
+  // tiles (chunk c -> XCD c % 8), so every XCD gets the same mix of tile
+  // sizes, and the M tiles of one weight tile stay on one XCD. Inside an XCD,
+  // position q goes to workgroup slot q % per_xcd in round q / per_xcd:
+  // consecutive tiles run at the same time on neighbouring workgroups.
+  constexpr int kChunk = kTileChunk;
   const int xcd = blockIdx.x & 7;
-  const int q = blockIdx.x >> 3;
+  const int slot = blockIdx.x >> 3;
   const int per_xcd = gridDim.x >> 3;
-  const int share = (total + 7) >> 3;
-  const int w_beg = xcd * share;
-  const int w_end = min(w_beg + share, total);
+  const int n_chunks = (total_tiles + kChunk - 1) / kChunk;
+  int xcd_tiles = 0;  // positions held by this XCD
+  if (xcd < n_chunks) {
+    const int mine = (n_chunks - xcd + 7) >> 3;
+    xcd_tiles = mine * kChunk;
+    if ((n_chunks - 1) % 8 == xcd) xcd_tiles -= n_chunks * kChunk - total_tiles;
+  }
+  if (slot >= xcd_tiles) return;  // uniform: no work for this workgroup
+  const int ntiles = (xcd_tiles - slot + per_xcd - 1) / per_xcd;
+  const int nk = p.K / BK;
+  const int total = ntiles * nk;  // stages in this workgroup's stream
 
-  // DMA lane mapping: row l/8 of an 8-row group g = wave + 4i (so g & 1 is
-  // wave & 1), logical chunk = physical chunk ^ swizzle(row)
-  const int dma_row = lane >> 3;
-  const int dma_chunk = (lane & 7) ^ dma_row ^ (wave & 1);
-  const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
-  const u32x4_t* lds4 = reinterpret_cast<const u32x4_t*>(lds);
-  const int nk = p.K / kBK;
-
-  for (int W = w_beg + q; W < w_end; W += per_xcd) {
+  struct Tile {
+    int g, m0, me, n0;  // rows [m0, me) of group g, output columns from n0
+  };
+  auto decode = [&](int t) -> Tile {
+    const int q = slot + t * per_xcd;
+    const int W = ((q / kChunk) * 8 + xcd) * kChunk + q % kChunk;
     int lo = 0, hi = G - 1;
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
       if (s_inc[mid] > W) hi = mid; else lo = mid + 1;
     }
-    const int g = lo;
-    const int local = W - (g > 0 ? s_inc[g - 1] : 0);
-    const int mb = s_mb[g], me = s_me[g];
-    const int mtiles = (me - mb + BM - 1) / BM;
-    const int nt = local / mtiles;
-    const int mt = local - nt * mtiles;
-    const int m0 = mb + mt * BM;
-    const int n0 = nt * OUT_N;
-    const uint16_t* Bg = p.B + (int64_t)g * p.b_group_stride;
+    const int local = W - (lo > 0 ? s_inc[lo - 1] : 0);
+    const int mb = s_mb[lo], gme = s_me[lo];
+    const int mt = (gme - mb + BM - 1) / BM;
+    const int nblk = (gme - mb + 31) / 32;
+    const int nt = local / mt;
+    const int mi = local - nt * mt;
+    const int m0 = mb + 32 * (mi * nblk / mt);
+    const int me = min(mb + 32 * ((mi + 1) * nblk / mt), gme);
+    return Tile{lo, m0, me, nt * OUT_N};
+  };
 
-    // ---- per-lane DMA source rows (out-of-range rows read a valid row; their
-    // results land in output rows/columns that are never stored)
-    const uint16_t* a_src[A_INSTS];
+  // DMA lane mapping: lane l lands at row l / CPR of its instruction's row group
+  // (RPI rows; group index wave + 4i), physical chunk l % CPR
+  const int dma_row = lane / CPR;
+  int dma_chunk;
+  if constexpr (CPR == 8) dma_chunk = (lane & 7) ^ dma_row ^ (wave & 1);
+  else dma_chunk = (lane & 3) ^ ((lane >> 4) & 3);
+  const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
+  const u32x4_t* lds4 = reinterpret_cast<const u32x4_t*>(lds);
+  const int row_limit = GATHER ? p.a_rows_limit : p.M;
+
+  // Gathered A rows: the row indices of all of this workgroup's tiles are
+  // staged once in the LDS past the ring, so the per-tile lookups are LDS reads
+  // (a vector load here would make its first use wait for every DMA issued
+  // before it). The launcher sizes the grid so that ntiles <= ROW_TILES.
+  // Rows past a group's end read a valid row whose results are never stored.
+  int* s_rows = reinterpret_cast<int*>(lds + Cfg::RING_BYTES / 2);
+  if constexpr (GATHER) {
+    if (ntiles > Cfg::ROW_TILES) return;  // excluded by the launcher
+    for (int idx = tid; idx < ntiles * BM; idx += Cfg::THREADS) {
+      const Tile t = decode(idx / BM);
+      const int m = t.m0 + idx % BM;
+      s_rows[idx] = p.a_rows[m < t.me ? m : t.m0];
+    }
+    __syncthreads();
+  }
+
+  // ---- issue side of the stage stream
+  const uint16_t* a_src[A_INSTS];
+  const uint16_t* b_src[B_INSTS];
+  auto set_sources = [&](int t_idx, const Tile& t) {
 #pragma unroll
     for (int i = 0; i < A_INSTS; ++i) {
-      const int m = m0 + 8 * (wave + 4 * i) + dma_row;
-      const int mm = m < me ? m : m0;
-      int row = mm;
-      if (p.a_rows != nullptr) {
-        row = p.a_rows[mm];
-        row = (row >= 0 && row < p.a_rows_limit) ? row : 0;
+      const int r = RPI * (wave + NW * i) + dma_row;
+      int row;
+      if constexpr (GATHER) {
+        row = s_rows[t_idx * BM + r];
+      } else {
+        const int m = t.m0 + r;
+        row = m < t.me ? m : t.m0;
       }
+      row = (row >= 0 && row < row_limit) ? row : 0;
       a_src[i] = p.A + (int64_t)row * p.lda + dma_chunk * 8;
     }
-    const uint16_t* b_src[B_INSTS];
+    const uint16_t* Bg = p.B + (int64_t)t.g * p.b_group_stride;
 #pragma unroll
     for (int i = 0; i < B_INSTS; ++i) {
-      const int r = 8 * (wave + 4 * i) + dma_row;
+      const int r = RPI * (wave + NW * i) + dma_row;
       int brow, col;
       if constexpr (SWIGLU) {
         const int wn = r / WN, w = r % WN;
         constexpr int half = WN / 2;
-        col = min(n0 + wn * half + (w % half), p.N - 1);
+        col = min(t.n0 + wn * half + (w % half), p.N - 1);
         brow = (w < half) ? col : p.up_row_offset + col;
       } else {
-        col = min(n0 + r, p.N - 1);
+        col = min(t.n0 + r, p.N - 1);
         brow = col;
       }
       b_src[i] = Bg + (int64_t)brow * p.ldb + dma_chunk * 8;
     }
+  };
+  auto issue = [&](int stage, int kt) {
+    const int koff = kt * BK;
+    const uint32_t sbase = lds_base + stage * Cfg::STAGE_BYTES;
+#pragma unroll
+    for (int i = 0; i < A_INSTS; ++i) {
+      const uint32_t dst = sbase + (wave + NW * i) * 1024;
+      __builtin_amdgcn_global_load_lds((global_void_t*)(a_src[i] + koff),
+                                       (lds_void_t*)(uintptr_t)dst, 16, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < B_INSTS; ++i) {
+      const uint32_t dst = sbase + Cfg::A_BYTES + (wave + NW * i) * 1024;
+      __builtin_amdgcn_global_load_lds((global_void_t*)(b_src[i] + koff),
+                                       (lds_void_t*)(uintptr_t)dst, 16, 0, 0);
+    }
+  };
 
-    auto issue = [&](int stage, int kt) {
-      const int koff = kt * kBK;
-      const uint32_t sbase = lds_base + stage * Cfg::STAGE_BYTES;
+  int is_tile = 0;      // tile whose stages are being issued
+  int is_kt = 0;        // its next stage
+  int gs_issue = 0;     // stages issued so far
+  set_sources(0, decode(0));
+  // Issues the next stage of the stream (if any), switching the DMA sources to
+  // the next tile after a tile's last stage.
+  auto issue_next = [&]() {
+    if (gs_issue >= total) return;
+    issue(gs_issue % kStages, is_kt);
+    ++gs_issue;
+    if (++is_kt == nk) {
+      is_kt = 0;
+      if (++is_tile < ntiles) set_sources(is_tile, decode(is_tile));
+    }
+  };
+
+  // ---- compute side
+  floatx16_t acc[TN][TM];
 #pragma unroll
-      for (int i = 0; i < A_INSTS; ++i) {
-        const uint32_t dst = sbase + (wave + 4 * i) * 1024;
-        __builtin_amdgcn_global_load_lds((global_void_t*)(a_src[i] + koff),
-                                         (lds_void_t*)(uintptr_t)dst, 16, 0, 0);
-      }
+  for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int i = 0; i < B_INSTS; ++i) {
-        const uint32_t dst = sbase + Cfg::A_BYTES + (wave + 4 * i) * 1024;
-        __builtin_amdgcn_global_load_lds((global_void_t*)(b_src[i] + koff),
-                                         (lds_void_t*)(uintptr_t)dst, 16, 0, 0);
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.f;
+
+  bf16x8_t fb[2][TN], fa[2][TM];
+  auto read_frags = [&](int set, int stage, int kk) {
+    const u32x4_t* As = lds4 + stage * (Cfg::STAGE_BYTES / 16);
+    const u32x4_t* Bs = As + Cfg::A_BYTES / 16;
+    const int ch = 2 * kk + (lane >> 5);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int rr = wave_n * WN + 32 * j + (lane & 31);
+      fb[set][j] = __builtin_bit_cast(bf16x8_t, Bs[lds_swz<CPR>(rr, ch)]);
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int rr = wave_m * WM + 32 * i + (lane & 31);
+      fa[set][i] = __builtin_bit_cast(bf16x8_t, As[lds_swz<CPR>(rr, ch)]);
+    }
+  };
+
+  auto active_blocks = [&](const Tile& t) {
+    return max(0, min(TM, (t.me - (t.m0 + wave_m * WM) + 31) / 32));
+  };
+
+  // prologue: STAGES stages in flight, stage 0 landed, its first fragments read
+#pragma unroll 1
+  for (int s = 0; s < kStages; ++s) issue_next();
+  wait_stage_landed<kStages - 1, NL>(gs_issue - 1);
+  lds_barrier();
+  read_frags(0, 0, 0);
+
+  int gc = 0;  // stages consumed
+  Tile ct = decode(0);
+#pragma unroll 1
+  for (int ct_idx = 0; ct_idx < ntiles; ++ct_idx) {
+    const int tma = active_blocks(ct);
+    // The K loop of one tile, for TMA active 32-row blocks of this wave (the
+    // blocks past the tile's rows are skipped). The variant is chosen per
+    // tile, so the accumulators never merge between variants inside the loop.
+    auto run_tile = [&](auto tma_c) {
+      constexpr int TMA = decltype(tma_c)::value;
+      constexpr int NREAD = TN + TM;
+      constexpr int NMFMA = TN * TMA;
+#pragma unroll 1
+      for (int kt = 0; kt < nk; ++kt, ++gc) {
+        const int stage = gc % kStages;
+        // K steps 0 .. KSTEPS-2: MFMAs of step kk, fragments of step kk+1
+#pragma unroll
+        for (int kk = 0; kk + 1 < KSTEPS; ++kk) {
+          read_frags((kk + 1) & 1, stage, kk + 1);
+#pragma unroll
+          for (int i = 0; i < TMA; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+              acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[kk & 1][j], fa[kk & 1][i],
+                                                                  acc[j][i], 0, 0, 0);
+        }
+#pragma unroll
+        for (int kk = 0; kk + 1 < KSTEPS; ++kk) sched_mfma_reads<NREAD, NMFMA>();
+        // Stage gc+1 must have landed (only later stages may be pending) and
+        // every wave must be done reading this stage's buffer before it is
+        // refilled with stage gc+STAGES.
+        if (gc + 1 < total) {
+          wait_stage_landed<kStages - 2, NL>(total - gc - 2);
+          __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS reads done
+          lds_barrier();
+          issue_next();
+        }
+        // last K step's MFMAs overlap the next stage's first fragment reads
+        // (after the last stage these are harmless, in-bounds LDS reads)
+        read_frags(0, (gc + 1) % kStages, 0);
+#pragma unroll
+        for (int i = 0; i < TMA; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                fb[(KSTEPS - 1) & 1][j], fa[(KSTEPS - 1) & 1][i], acc[j][i], 0, 0, 0);
+        sched_mfma_reads<NREAD, NMFMA>();
       }
     };
+    dispatch_active<TM>(tma, run_tile);
 
-    int tm_active = (me - (m0 + wave_m * WM) + 31) / 32;
-    tm_active = max(0, min(TM, tm_active));
-
-    floatx16_t acc[TN][TM];
+    // ---- epilogue (the next tile's first stages are already in flight):
+    // lane owns token row m = ... + (lane & 31) and 4 consecutive output
+    // columns per 4-register group
+    {
+      constexpr int JN = SWIGLU ? TN / 2 : TN;
+      constexpr int WOUT = SWIGLU ? WN / 2 : WN;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        if (i >= tma) continue;
+        const int m = ct.m0 + wave_m * WM + 32 * i + (lane & 31);
+        if (m >= ct.me) continue;
+        uint16_t* crow = p.C + (int64_t)m * p.ldc;
+#pragma unroll
+        for (int j = 0; j < JN; ++j) {
+#pragma unroll
+          for (int qg = 0; qg < 4; ++qg) {
+            const int nb = ct.n0 + wave_n * WOUT + 32 * j + 8 * qg + 4 * (lane >> 5);
+            float v[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              if constexpr (SWIGLU)
+                v[c] = silu_f(acc_read(acc[j][i][4 * qg + c])) *
+                       acc_read(acc[j + TN / 2][i][4 * qg + c]);
+              else
+                v[c] = acc_read(acc[j][i][4 * qg + c]);
+            }
+            if (nb + 3 < p.N) {
+              u32x2_t o;
+              o[0] = pack_bf16x2(v[0], v[1]);
+              o[1] = pack_bf16x2(v[2], v[3]);
+              *reinterpret_cast<u32x2_t*>(crow + nb) = o;
+            } else {
+#pragma unroll
+              for (int c = 0; c < 4; ++c)
+                if (nb + c < p.N) crow[nb + c] = f32_to_bf16(v[c]);
+            }
+          }
+        }
+      }
+    }
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.f;
-
-    // prologue: stages 0 .. kStages-2 in flight
-#pragma unroll
-    for (int s = 0; s < kStages - 1; ++s)
-      if (s < nk) issue(s, s);
-
-    // K loop, specialised on the number of active 32-row blocks of this wave
-    // (TMA) so the common full-tile case has no control flow around the MFMAs.
-    auto mainloop = [&](auto tma_c) {
-      constexpr int TMA = decltype(tma_c)::value;
-      for (int kt = 0; kt < nk; ++kt) {
-        // stage kt has landed when at most the loads of the stages issued after
-        // it (min(kStages - 2, nk - 1 - kt) of them) are pending
-        wait_stage_landed<kStages - 2, NL>(nk - 1 - kt);
-        lds_barrier();
-        if (kt + kStages - 1 < nk) issue((kt + kStages - 1) % kStages, kt + kStages - 1);
-        if constexpr (TMA > 0) {
-          const int stage = kt % kStages;
-          const u32x4_t* As = lds4 + stage * (Cfg::STAGE_BYTES / 16);
-          const u32x4_t* Bs = As + Cfg::A_BYTES / 16;
-          // fragments of K-step kk are read into register set kk&1 while the
-          // MFMAs of step kk-1 run from the other set
-          bf16x8_t fb[2][TN], fa[2][TMA];
-          auto read_frags = [&](int set, int kk) {
-            const int ch = 2 * kk + (lane >> 5);
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
-              const int rr = wave_n * WN + 32 * j + (lane & 31);
-              fb[set][j] = __builtin_bit_cast(bf16x8_t, Bs[lds_swz(rr, ch)]);
-            }
-#pragma unroll
-            for (int i = 0; i < TMA; ++i) {
-              const int rr = wave_m * WM + 32 * i + (lane & 31);
-              fa[set][i] = __builtin_bit_cast(bf16x8_t, As[lds_swz(rr, ch)]);
-            }
-          };
-          constexpr int KSTEPS = kBK / 16;
-          constexpr int NREAD = TN + TMA;   // ds_read_b128 per K-step
-          constexpr int NMFMA = TN * TMA;   // MFMAs per K-step
-          read_frags(0, 0);
-#pragma unroll
-          for (int kk = 0; kk < KSTEPS; ++kk) {
-            if (kk + 1 < KSTEPS) read_frags((kk + 1) & 1, kk + 1);
-#pragma unroll
-            for (int i = 0; i < TMA; ++i)
-#pragma unroll
-              for (int j = 0; j < TN; ++j)
-                acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[kk & 1][j], fa[kk & 1][i],
-                                                                    acc[j][i], 0, 0, 0);
-          }
-          // schedule: step-0 reads, then each step's MFMAs with the next step's
-          // reads front-loaded (two reads after each of the first MFMAs), so the
-          // reads have most of the step's MFMAs to land
-          __builtin_amdgcn_sched_group_barrier(0x100, NREAD, 0);
-#pragma unroll
-          for (int kk = 0; kk < KSTEPS; ++kk) {
-            if (kk + 1 < KSTEPS) {
-              sched_mfma_reads<NREAD, NMFMA>();
-            } else {
-              __builtin_amdgcn_sched_group_barrier(0x008, NMFMA, 0);
-            }
-          }
-        }
-      }
-    };
-    dispatch_count<TM>(tm_active, mainloop);
-    // all waves are done reading the ring before the next tile's prologue DMA
-    __syncthreads();
-
-    // ---- epilogue: lane owns token row m = ... + (lane & 31) and 4 consecutive
-    // output columns per 4-register group
-    constexpr int JN = SWIGLU ? TN / 2 : TN;
-    constexpr int WOUT = SWIGLU ? WN / 2 : WN;
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      if (i >= tm_active) continue;
-      const int m = m0 + wave_m * WM + 32 * i + (lane & 31);
-      if (m >= me) continue;
-      uint16_t* crow = p.C + (int64_t)m * p.ldc;
-#pragma unroll
-      for (int j = 0; j < JN; ++j) {
-#pragma unroll
-        for (int qg = 0; qg < 4; ++qg) {
-          const int nb = n0 + wave_n * WOUT + 32 * j + 8 * qg + 4 * (lane >> 5);
-          float v[4];
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            if constexpr (SWIGLU)
-              v[c] = silu_f(acc[j][i][4 * qg + c]) * acc[j + TN / 2][i][4 * qg + c];
-            else
-              v[c] = acc[j][i][4 * qg + c];
-          }
-          if (nb + 3 < p.N) {
-            u32x2_t o;
-            o[0] = pack_bf16x2(v[0], v[1]);
-            o[1] = pack_bf16x2(v[2], v[3]);
-            *reinterpret_cast<u32x2_t*>(crow + nb) = o;
-          } else {
-#pragma unroll
-            for (int c = 0; c < 4; ++c)
-              if (nb + c < p.N) crow[nb + c] = f32_to_bf16(v[c]);
-          }
-        }
-      }
-    }
+    if (ct_idx + 1 < ntiles) ct = decode(ct_idx + 1);
   }
 }
 
@@ -411,10 +542,11 @@ static int num_cus() {
   return cached[dev];
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, bool SWIGLU>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int BK, int STAGES, bool SWIGLU,
+          bool GATHER>
 static int launch_grouped_gemm(const GemmArgs& a, hipStream_t st) {
-  using Cfg = GemmCfg<BM, BN, WAVES_M, WAVES_N, STAGES, SWIGLU>;
-  auto kern = grouped_gemm_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, SWIGLU>;
+  using Cfg = GemmCfg<BM, BN, WAVES_M, WAVES_N, BK, STAGES, SWIGLU>;
+  auto kern = grouped_gemm_kernel<BM, BN, WAVES_M, WAVES_N, BK, STAGES, SWIGLU, GATHER>;
   static std::once_flag once;
   std::call_once(once, [&] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -425,7 +557,16 @@ static int launch_grouped_gemm(const GemmArgs& a, hipStream_t st) {
   const int64_t upper = ((int64_t)(a.M + BM - 1) / BM + (a.offsets ? G : 0)) * nt;
   int64_t nwg = std::min<int64_t>(upper, (int64_t)num_cus());
   nwg = std::max<int64_t>(8, (nwg + 7) / 8 * 8);
-  hipLaunchKernelGGL(kern, dim3((unsigned)nwg), dim3(kGemmThreads), Cfg::LDS_BYTES, st, a);
+  if (GATHER) {
+    // every workgroup's tile count must fit the LDS row table: an XCD holds
+    // at most ceil(chunks / 8) chunks of kTileChunk tiles, spread over nwg / 8
+    // workgroups
+    const int64_t chunks = (upper + kTileChunk - 1) / kTileChunk;
+    const int64_t xcd_max = (chunks + 7) / 8 * kTileChunk;
+    const int64_t per_xcd_min = (xcd_max + Cfg::ROW_TILES - 1) / Cfg::ROW_TILES;
+    nwg = std::max<int64_t>(nwg, 8 * per_xcd_min);
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)nwg), dim3(Cfg::THREADS), Cfg::LDS_BYTES, st, a);
   return check_launch("grouped_gemm_kernel");
 }
 
@@ -435,8 +576,8 @@ static int validate_gemm(const GemmArgs& a, const char* who) {
     snprintf(buf, sizeof buf, "%s: invalid sizes M=%d N=%d K=%d", who, a.M, a.N, a.K);
     return fail(DSK_ERR_INVALID_ARG, buf);
   }
-  if (a.K % kBK != 0) {
-    snprintf(buf, sizeof buf, "%s: K=%d must be a multiple of %d", who, a.K, kBK);
+  if (a.K % DSK_GEMM_BK != 0) {
+    snprintf(buf, sizeof buf, "%s: K=%d must be a multiple of %d", who, a.K, DSK_GEMM_BK);
     return fail(DSK_ERR_INVALID_ARG, buf);
   }
   if (a.offsets != nullptr && (a.G < 1 || a.G > kMaxGroups)) {
@@ -453,15 +594,21 @@ static int validate_gemm(const GemmArgs& a, const char* who) {
   return DSK_OK;
 }
 
-// Tile choice: 128 tokens x 256 weight rows, waves side by side along the
-// weight rows (each wave 128 x 64), so a wave can skip the 32-row blocks past
+// Tile choice: 256 tokens x 256 weight rows, waves side by side along the
+// weight rows (each wave 256 x 64), so a wave can skip the 32-row blocks past
 // the end of its group.
 int run_gemm(const GemmArgs& a, bool swiglu, hipStream_t st) {
   if (a.M == 0) return DSK_OK;
-  constexpr int BM = DSK_GEMM_BM, BN = DSK_GEMM_BN, WAVES_M = DSK_GEMM_WAVES_M;
-  constexpr int STAGES = DSK_GEMM_STAGES;
-  if (swiglu) return launch_grouped_gemm<BM, BN, WAVES_M, 4 / WAVES_M, STAGES, true>(a, st);
-  return launch_grouped_gemm<BM, BN, WAVES_M, 4 / WAVES_M, STAGES, false>(a, st);
+  constexpr int BM = DSK_GEMM_BM, BN = DSK_GEMM_BN, WM = DSK_GEMM_WAVES_M;
+  constexpr int BK = DSK_GEMM_BK, ST = DSK_GEMM_STAGES;
+  constexpr int WN = DSK_GEMM_WAVES_N;
+  const bool gather = a.a_rows != nullptr;
+  if (swiglu) {
+    if (gather) return launch_grouped_gemm<BM, BN, WM, WN, BK, ST, true, true>(a, st);
+    return launch_grouped_gemm<BM, BN, WM, WN, BK, ST, true, false>(a, st);
+  }
+  if (gather) return launch_grouped_gemm<BM, BN, WM, WN, BK, ST, false, true>(a, st);
+  return launch_grouped_gemm<BM, BN, WM, WN, BK, ST, false, false>(a, st);
 }
 
 int zero_uncovered_rows(uint16_t* C, int64_t ldc, int M, int N, const int32_t* offsets,

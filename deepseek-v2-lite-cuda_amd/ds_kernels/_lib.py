@@ -13,7 +13,7 @@ import os
 import torch  # noqa: F401  (must be loaded before libdsk.so, see above)
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.environ.get("DSK_LIB", os.path.join(_HERE, "libdsk.so"))
+LIB_PATH = os.environ.get("DSK_LIB") or os.path.join(_HERE, "libdsk.so")
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
