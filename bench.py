@@ -18,7 +18,7 @@ Also reported on the same line:
   cpu_baseline  the CPU oracle (numpy restatement of DeepSeekMoE.forward) timed
                 on a bounded sample (config 0, T=64 fp32) on this host's cores.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--profile]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--profile | --decode-only T]
 """
 from __future__ import annotations
 
@@ -73,8 +73,7 @@ def bench_prefill(dsk, syn, torch, F, W, packed, T, steps, warmup, ev):
     dev = w1.device
     wg = W.wg.to(torch.bfloat16).to(dev)
     x = syn.tokens(T).to(torch.bfloat16).to(dev)
-    I = w2.shape[2]
-    H = w2.shape[1]
+    H, I = 2048, 1408
     ws = torch.empty(dsk.lib.dsk_moe_fused_workspace_size(T, 64, 6, nsh, H, I),
                      dtype=torch.uint8, device=dev)
     events = [ev.create(5) for _ in range(steps)]
@@ -112,7 +111,7 @@ def bench_decode(dsk, syn, torch, F, W, packed, T, steps, ev, copies):
     wg = W.wg.to(torch.bfloat16).to(dev)
     bias = syn.zipf_router_bias().to(dev)
     x = syn.tokens(T).to(torch.bfloat16).to(dev)
-    I, H = w2.shape[2], w2.shape[1]
+    H, I = 2048, 1408
     ws = torch.empty(dsk.lib.dsk_moe_fused_workspace_size(T, 64, 6, nsh, H, I),
                      dtype=torch.uint8, device=dev)
 
@@ -236,6 +235,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--profile", action="store_true",
                     help="prefill steps only (no decode sweep, no CPU baseline)")
+    ap.add_argument("--decode-only", type=int, default=0, metavar="T",
+                    help="only the decode-shaped layer at T tokens (for profiling)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only the 1 GiB device copy used to scale the HBM counters")
     args = ap.parse_args()
@@ -257,8 +258,18 @@ def main():
     torch.cuda.set_device(dev)
     print("bench: generating synthetic weights", file=sys.stderr, flush=True)
     W = syn.moe_weights()
-    packed = dsk.pack_tensors(W.gates, W.ups, W.downs, device=dev, shared=W.shared)
+    w1, w2, nsh = dsk.pack_tensors(W.gates, W.ups, W.downs, device=dev, shared=W.shared)
+    # the fused layer's native layout: fragment-tiled expert weights
+    packed = (dsk.tile_weights(w1), dsk.tile_weights(w2), nsh)
+    del w1, w2
     ev = HipEvents()
+
+    if args.decode_only:
+        w1, w2, nsh = packed
+        copies = [(w1, w2)] + [(w1.clone(), w2.clone()) for _ in range(3)]
+        print(json.dumps(bench_decode(dsk, syn, torch, F, W, packed, args.decode_only,
+                                      args.decode_steps, ev, copies)), flush=True)
+        return
 
     print("bench: prefill", file=sys.stderr, flush=True)
     pre = bench_prefill(dsk, syn, torch, F, W, packed, args.tokens, args.steps, args.warmup, ev)

@@ -20,6 +20,10 @@ struct GemmArgs {
   int G;
   int M, N, K;             // N = output columns (SwiGLU: intermediate size)
   int up_row_offset;       // SwiGLU: first up row inside a group's weight
+  int max_group_rows;      // upper bound on any group's row count known to the host
+                           // (0: unknown, M is used); selects the small-group kernel
+  int b_tiled;             // B stored as MFMA fragments (see the fragment-tiled layout in
+                           // dsk.h); ldb is then unused
 };
 
 int run_gemm(const GemmArgs& a, bool swiglu, hipStream_t st);

@@ -187,7 +187,7 @@ __device__ __forceinline__ int lds_swz(int row, int chunk) {
 }
 
 template <int BM, int BN, int WAVES_M, int WAVES_N, int BK, int STAGES, bool SWIGLU,
-          bool GATHER>
+          bool GATHER, bool TILED>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void grouped_gemm_kernel(GemmArgs p) {
   using Cfg = GemmCfg<BM, BN, WAVES_M, WAVES_N, BK, STAGES, SWIGLU>;
   constexpr int kStages = STAGES;
@@ -329,22 +329,40 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void grouped_gemm_kernel
     const uint16_t* Bg = p.B + (int64_t)t.g * p.b_group_stride;
 #pragma unroll
     for (int i = 0; i < B_INSTS; ++i) {
-      const int r = RPI * (wave + NW * i) + dma_row;
-      int brow, col;
-      if constexpr (SWIGLU) {
-        const int wn = r / WN, w = r % WN;
-        constexpr int half = WN / 2;
-        col = min(t.n0 + wn * half + (w % half), p.N - 1);
-        brow = (w < half) ? col : p.up_row_offset + col;
+      if constexpr (TILED) {
+        // one 1 KB fragment (32 weight rows x 16 k) per instruction: local
+        // fragment f = row block * (BK/16) + k step
+        const int f = wave + NW * i;
+        const int rbl = f / (BK / 16), ksl = f % (BK / 16);
+        int rb;
+        if constexpr (SWIGLU) {
+          const int wn = rbl / TN, wb = rbl % TN;
+          const int cb = min(t.n0 / 32 + wn * (TN / 2) + wb % (TN / 2), p.N / 32 - 1);
+          rb = wb < TN / 2 ? cb : p.up_row_offset / 32 + cb;
+        } else {
+          rb = min(t.n0 / 32 + rbl, p.N / 32 - 1);
+        }
+        b_src[i] = Bg + ((int64_t)rb * (p.K / 16) + ksl) * 512 + lane * 8;
       } else {
-        col = min(t.n0 + r, p.N - 1);
-        brow = col;
+        const int r = RPI * (wave + NW * i) + dma_row;
+        int brow, col;
+        if constexpr (SWIGLU) {
+          const int wn = r / WN, w = r % WN;
+          constexpr int half = WN / 2;
+          col = min(t.n0 + wn * half + (w % half), p.N - 1);
+          brow = (w < half) ? col : p.up_row_offset + col;
+        } else {
+          col = min(t.n0 + r, p.N - 1);
+          brow = col;
+        }
+        b_src[i] = Bg + (int64_t)brow * p.ldb + dma_chunk * 8;
       }
-      b_src[i] = Bg + (int64_t)brow * p.ldb + dma_chunk * 8;
     }
   };
   auto issue = [&](int stage, int kt) {
     const int koff = kt * BK;
+    // tiled weights: a stage is BK/16 consecutive fragments of 512 elements
+    const int bkoff = TILED ? kt * (BK / 16) * 512 : koff;
     const uint32_t sbase = lds_base + stage * Cfg::STAGE_BYTES;
 #pragma unroll
     for (int i = 0; i < A_INSTS; ++i) {
@@ -355,7 +373,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void grouped_gemm_kernel
 #pragma unroll
     for (int i = 0; i < B_INSTS; ++i) {
       const uint32_t dst = sbase + Cfg::A_BYTES + (wave + NW * i) * 1024;
-      __builtin_amdgcn_global_load_lds((global_void_t*)(b_src[i] + koff),
+      __builtin_amdgcn_global_load_lds((global_void_t*)(b_src[i] + bkoff),
                                        (lds_void_t*)(uintptr_t)dst, 16, 0, 0);
     }
   };
@@ -392,8 +410,13 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void grouped_gemm_kernel
     const int ch = 2 * kk + (lane >> 5);
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      const int rr = wave_n * WN + 32 * j + (lane & 31);
-      fb[set][j] = __builtin_bit_cast(bf16x8_t, Bs[lds_swz<CPR>(rr, ch)]);
+      if constexpr (TILED) {
+        fb[set][j] = __builtin_bit_cast(
+            bf16x8_t, Bs[((wave_n * TN + j) * (BK / 16) + kk) * 64 + lane]);
+      } else {
+        const int rr = wave_n * WN + 32 * j + (lane & 31);
+        fb[set][j] = __builtin_bit_cast(bf16x8_t, Bs[lds_swz<CPR>(rr, ch)]);
+      }
     }
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
@@ -514,6 +537,265 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void grouped_gemm_kernel
   }
 }
 
+// ------------------------------------------------------- small groups ----
+// Grouped GEMM for groups of at most 32*MT rows (decode-shaped layers: T <= 64
+// tokens, so every expert holds at most T rows). The work is streaming the
+// active experts' weights once from HBM, so the kernel is built for memory
+// parallelism rather than reuse:
+//   * one workgroup per (group, 64 weight rows): for SwiGLU the 32 gate rows
+//     and the matching 32 up rows of 32 output columns, otherwise 64
+//     consecutive rows; workgroups of empty groups exit at once, so idle
+//     experts cost no bandwidth;
+//   * the 4 waves split K four ways; each lane loads its MFMA fragments of
+//     weights and tokens straight from global memory into registers (no LDS,
+//     no barrier in the K loop), one batch of K steps ahead of the MFMAs, so
+//     even a handful of active experts keeps enough loads in flight for HBM
+//     latency; with fragment-tiled weights every load is 1 KB contiguous;
+//   * the partial sums meet in LDS once at the end, in a fixed order (waves
+//     1-3 into wave 0), and wave 0 applies the epilogue (SwiGLU from fp32
+//     accumulators).
+// The weights are MFMA operand A and the tokens operand B, as in the large
+// kernel, so the output layout per lane is the same (4 consecutive columns).
+constexpr int kSkinnyWaves = 4;  // waves per workgroup, each one slice of K
+constexpr int kSkinnyThreads = 64 * kSkinnyWaves;
+constexpr int kSkinnyMaxRows = 64;  // largest group the small-group kernel is chosen for
+constexpr int kSkinnyBatch = 4;  // K steps (of 16) per load batch
+
+template <int MT, bool SWIGLU, bool GATHER, bool TILED>
+__global__ __launch_bounds__(kSkinnyThreads) void skinny_gemm_kernel(GemmArgs p, int n_blocks) {
+  constexpr int NB = 2;  // 32-row weight blocks per workgroup
+  // partial sums of the upper half of the waves (8 waves), then of waves 1..3
+  __shared__ floatx4_t red[kSkinnyWaves == 8 ? 4 : 3][NB][MT][4][64];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = blockIdx.x / n_blocks;
+  const int nb = blockIdx.x - g * n_blocks;
+  int mb = 0, me = p.M;
+  if (p.offsets != nullptr) {
+    mb = min(max(p.offsets[g], 0), p.M);
+    me = min(max(p.offsets[g + 1], mb), p.M);
+  }
+  if (mb >= me) return;  // uniform: empty group
+
+  const int r32 = lane & 31;
+  const int h = lane >> 5;
+  // Loads address a uniform base (scalar registers) plus a 32-bit per-lane
+  // byte offset, so each load needs one VGPR of address and the K steps of a
+  // batch become immediate offsets. Offsets stay below 4 GiB: one group's
+  // weights, and at most 64 token rows of A.
+  const char* Bg = reinterpret_cast<const char*>(p.B + (int64_t)g * p.b_group_stride);
+  const char* Ab = reinterpret_cast<const char*>(p.A);
+  // K steps (of 16) of this wave: an even split of K/16 over the waves
+  const int ksteps = p.K / 16;
+  const int s_beg = wave * ksteps / kSkinnyWaves;
+  const int nsteps = (wave + 1) * ksteps / kSkinnyWaves - s_beg;
+  const int k_beg = s_beg * 16;
+  // Byte offset of this lane's fragment data at k_beg in each weight block.
+  // Row-major weights: row r32 of the block, 32 bytes per K step (each load
+  // instruction touches 32 rows). Tiled weights: the 1 KB fragment of the
+  // block at this K step, lane-contiguous, 1 KB per K step (each load
+  // instruction reads 1 KB of consecutive bytes).
+  constexpr uint32_t kStepBytes = TILED ? 1024 : 32;
+  uint32_t woff[NB];
+#pragma unroll
+  for (int blk = 0; blk < NB; ++blk) {
+    if constexpr (TILED) {
+      int rb;
+      if constexpr (SWIGLU) {
+        const int cb = min(nb, p.N / 32 - 1);
+        rb = blk == 0 ? cb : p.up_row_offset / 32 + cb;
+      } else {
+        rb = min(nb * 2 + blk, p.N / 32 - 1);
+      }
+      woff[blk] = (uint32_t)((((int64_t)rb * (p.K / 16) + k_beg / 16) * 512 + lane * 8) * 2);
+    } else {
+      int row;
+      if constexpr (SWIGLU) {
+        const int col = min(nb * 32 + r32, p.N - 1);
+        row = blk == 0 ? col : p.up_row_offset + col;
+      } else {
+        row = min(nb * 64 + blk * 32 + r32, p.N - 1);
+      }
+      woff[blk] = (uint32_t)(((int64_t)row * p.ldb + 8 * h + k_beg) * 2);
+    }
+  }
+  const int row_limit = GATHER ? p.a_rows_limit : p.M;
+
+  for (int m0 = mb; m0 < me; m0 += 32 * MT) {
+    uint32_t toff[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = m0 + mt * 32 + r32;
+      const int mm = m < me ? m : m0;
+      int row = GATHER ? p.a_rows[mm] : mm;
+      row = (row >= 0 && row < row_limit) ? row : 0;
+      toff[mt] = (uint32_t)(((int64_t)row * p.lda + 8 * h + k_beg) * 2);
+    }
+    floatx16_t acc[NB][MT];
+#pragma unroll
+    for (int blk = 0; blk < NB; ++blk)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[blk][mt][r] = 0.f;
+
+    // Software pipeline over batches of kSkinnyBatch K steps: the loads of
+    // batch b+1 are in flight while batch b's MFMAs run (two register
+    // buffers, unrolled by two so they are indexed statically). The
+    // scheduling barriers keep the compiler from interleaving loads and
+    // MFMAs, which would leave only a few loads in flight.
+    constexpr int U = kSkinnyBatch;
+    bf16x8_t wa[U][NB], ta[U][MT], wb[U][NB], tb[U][MT];
+    auto load = [&](bf16x8_t (&wf)[U][NB], bf16x8_t (&tf)[U][MT], int s) {
+      const uint32_t ks = (uint32_t)s * 32;  // byte offset of K step s in a token row
+      const uint32_t kw_s = (uint32_t)s * kStepBytes;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+#pragma unroll
+        for (int blk = 0; blk < NB; ++blk)
+          wf[u][blk] = __builtin_nontemporal_load(  // read once: stream past the caches
+              reinterpret_cast<const bf16x8_t*>(Bg + (woff[blk] + kw_s) + kStepBytes * u));
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          tf[u][mt] = *reinterpret_cast<const bf16x8_t*>(Ab + (toff[mt] + ks) + 32 * u);
+      }
+    };
+    auto compute = [&](const bf16x8_t (&wf)[U][NB], const bf16x8_t (&tf)[U][MT], int n) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (u >= n) break;
+#pragma unroll
+        for (int blk = 0; blk < NB; ++blk)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            acc[blk][mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[u][blk], tf[u][mt],
+                                                                   acc[blk][mt], 0, 0, 0);
+      }
+    };
+    const int nbatch = nsteps / U;
+    if (nbatch > 0) {
+      load(wa, ta, 0);
+      int b = 0;
+      for (; b + 2 <= nbatch; b += 2) {
+        load(wb, tb, (b + 1) * U);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(wa, ta, U);
+        __builtin_amdgcn_sched_barrier(0);
+        // past the last batch this reloads the last one (cache hits, unused),
+        // which keeps the loop free of conditional loads
+        load(wa, ta, min(b + 2, nbatch - 1) * U);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(wb, tb, U);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (b < nbatch) compute(wa, ta, U);
+    }
+    // remaining K steps (nsteps not a multiple of the batch)
+    for (int s = nbatch * U; s < nsteps; ++s) {
+      bf16x8_t w1[1][NB], t1[1][MT];
+      const uint32_t ks = (uint32_t)s * 32;
+#pragma unroll
+      for (int blk = 0; blk < NB; ++blk)
+        w1[0][blk] = __builtin_nontemporal_load(
+            reinterpret_cast<const bf16x8_t*>(Bg + (woff[blk] + s * kStepBytes)));
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        t1[0][mt] = *reinterpret_cast<const bf16x8_t*>(Ab + (toff[mt] + ks));
+#pragma unroll
+      for (int blk = 0; blk < NB; ++blk)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          acc[blk][mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w1[0][blk], t1[0][mt],
+                                                                 acc[blk][mt], 0, 0, 0);
+    }
+
+    // ---- reduce the K slices (upper half of the waves into the lower half,
+    // then waves 1..3 into wave 0), epilogue by wave 0 one group of 4 output
+    // columns at a time, so few values are live at once
+    auto stash = [&](int slot) {
+#pragma unroll
+      for (int blk = 0; blk < NB; ++blk)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int qg = 0; qg < 4; ++qg) {
+            floatx4_t v;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) v[c] = acc[blk][mt][4 * qg + c];
+            red[slot][blk][mt][qg][lane] = v;
+          }
+    };
+    static_assert(kSkinnyWaves == 4 || kSkinnyWaves == 8, "reduction written for 4 or 8 waves");
+    if constexpr (kSkinnyWaves == 8) {
+      if (wave >= 4) stash(wave - 4);
+      __syncthreads();
+      if (wave < 4) {
+#pragma unroll
+      for (int blk = 0; blk < NB; ++blk)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int qg = 0; qg < 4; ++qg) {
+            const floatx4_t v = red[wave][blk][mt][qg][lane];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[blk][mt][4 * qg + c] += v[c];
+          }
+      }
+      __syncthreads();
+    }
+    if (wave >= 1 && wave < 4) stash(wave - 1);
+    __syncthreads();
+    if (wave == 0) {
+      auto total = [&](int blk, int mt, int qg) {
+        floatx4_t v = red[0][blk][mt][qg][lane] + red[1][blk][mt][qg][lane] +
+                      red[2][blk][mt][qg][lane];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[c] += acc_read(acc[blk][mt][4 * qg + c]);
+        return v;
+      };
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int m = m0 + mt * 32 + r32;
+        uint16_t* crow = p.C + (int64_t)m * p.ldc;
+        constexpr int JN = SWIGLU ? 1 : NB;
+#pragma unroll
+        for (int j = 0; j < JN; ++j) {
+#pragma unroll
+          for (int qg = 0; qg < 4; ++qg) {
+            const int nbase = SWIGLU ? nb * 32 : nb * 64 + j * 32;
+            const int n = nbase + 8 * qg + 4 * h;
+            float v[4];
+            if constexpr (SWIGLU) {
+              const floatx4_t gt = total(0, mt, qg), up = total(1, mt, qg);
+#pragma unroll
+              for (int c = 0; c < 4; ++c) v[c] = silu_f(gt[c]) * up[c];
+            } else {
+              const floatx4_t t = total(j, mt, qg);
+#pragma unroll
+              for (int c = 0; c < 4; ++c) v[c] = t[c];
+            }
+            if (m < me) {
+              if (n + 3 < p.N) {
+                u32x2_t o;
+                o[0] = pack_bf16x2(v[0], v[1]);
+                o[1] = pack_bf16x2(v[2], v[3]);
+                *reinterpret_cast<u32x2_t*>(crow + n) = o;
+              } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                  if (n + c < p.N) crow[n + c] = f32_to_bf16(v[c]);
+              }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+      }
+    }
+    __syncthreads();  // red is reused by the next row chunk
+  }
+}
+
 // Zero the output rows that no group covers: [0, offsets[0]) and [offsets[G], M).
 __global__ __launch_bounds__(256) void zero_uncovered_rows_kernel(
     uint16_t* __restrict__ C, int64_t ldc, int M, int N,
@@ -543,10 +825,10 @@ static int num_cus() {
 }
 
 template <int BM, int BN, int WAVES_M, int WAVES_N, int BK, int STAGES, bool SWIGLU,
-          bool GATHER>
+          bool GATHER, bool TILED>
 static int launch_grouped_gemm(const GemmArgs& a, hipStream_t st) {
   using Cfg = GemmCfg<BM, BN, WAVES_M, WAVES_N, BK, STAGES, SWIGLU>;
-  auto kern = grouped_gemm_kernel<BM, BN, WAVES_M, WAVES_N, BK, STAGES, SWIGLU, GATHER>;
+  auto kern = grouped_gemm_kernel<BM, BN, WAVES_M, WAVES_N, BK, STAGES, SWIGLU, GATHER, TILED>;
   static std::once_flag once;
   std::call_once(once, [&] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -570,6 +852,22 @@ static int launch_grouped_gemm(const GemmArgs& a, hipStream_t st) {
   return check_launch("grouped_gemm_kernel");
 }
 
+template <int MT, bool SWIGLU, bool GATHER, bool TILED>
+static int launch_skinny_gemm(const GemmArgs& a, hipStream_t st) {
+  const int G = a.offsets != nullptr ? a.G : 1;
+  const int n_blocks = SWIGLU ? (a.N + 31) / 32 : (a.N + 63) / 64;
+  const int64_t grid = (int64_t)G * n_blocks;
+  hipLaunchKernelGGL((skinny_gemm_kernel<MT, SWIGLU, GATHER, TILED>), dim3((unsigned)grid),
+                     dim3(kSkinnyThreads), 0, st, a, n_blocks);
+  return check_launch("skinny_gemm_kernel");
+}
+
+template <bool SWIGLU, bool GATHER, bool TILED>
+static int launch_skinny(const GemmArgs& a, int rows, hipStream_t st) {
+  if (rows <= 32) return launch_skinny_gemm<1, SWIGLU, GATHER, TILED>(a, st);
+  return launch_skinny_gemm<2, SWIGLU, GATHER, TILED>(a, st);
+}
+
 static int validate_gemm(const GemmArgs& a, const char* who) {
   char buf[256];
   if (a.M < 0 || a.N <= 0 || a.K <= 0) {
@@ -589,26 +887,36 @@ static int validate_gemm(const GemmArgs& a, const char* who) {
     return fail(DSK_ERR_ALIGNMENT, std::string(who) + ": A/B rows must be 16-byte aligned");
   if ((reinterpret_cast<uintptr_t>(a.C) & 7u) || a.ldc % 4)
     return fail(DSK_ERR_ALIGNMENT, std::string(who) + ": C rows must be 8-byte aligned");
-  if (a.lda < a.K || a.ldb < a.K)
+  if (a.lda < a.K || (!a.b_tiled && a.ldb < a.K))
     return fail(DSK_ERR_INVALID_ARG, std::string(who) + ": leading dimension < K");
+  if (a.b_tiled && (a.N % 32 || a.up_row_offset % 32))
+    return fail(DSK_ERR_INVALID_ARG,
+                std::string(who) + ": tiled weights need N and the up-row offset in multiples of 32");
   return DSK_OK;
 }
 
-// Tile choice: 256 tokens x 256 weight rows, waves side by side along the
-// weight rows (each wave 256 x 64), so a wave can skip the 32-row blocks past
-// the end of its group.
-int run_gemm(const GemmArgs& a, bool swiglu, hipStream_t st) {
-  if (a.M == 0) return DSK_OK;
+// Kernel choice: groups known to hold at most 64 rows (decode) go to the
+// weight-streaming kernel, everything else to the 256 x 256 tile kernel.
+template <bool SWIGLU, bool GATHER, bool TILED>
+static int run_gemm_t(const GemmArgs& a, hipStream_t st) {
+  // groups of at most 64 rows (decode): weight streaming kernel
+  const int rows = a.max_group_rows > 0 ? std::min(a.max_group_rows, a.M) : a.M;
+  if (rows <= kSkinnyMaxRows) return launch_skinny<SWIGLU, GATHER, TILED>(a, rows, st);
   constexpr int BM = DSK_GEMM_BM, BN = DSK_GEMM_BN, WM = DSK_GEMM_WAVES_M;
   constexpr int BK = DSK_GEMM_BK, ST = DSK_GEMM_STAGES;
   constexpr int WN = DSK_GEMM_WAVES_N;
-  const bool gather = a.a_rows != nullptr;
-  if (swiglu) {
-    if (gather) return launch_grouped_gemm<BM, BN, WM, WN, BK, ST, true, true>(a, st);
-    return launch_grouped_gemm<BM, BN, WM, WN, BK, ST, true, false>(a, st);
+  return launch_grouped_gemm<BM, BN, WM, WN, BK, ST, SWIGLU, GATHER, TILED>(a, st);
+}
+
+int run_gemm(const GemmArgs& a, bool swiglu, hipStream_t st) {
+  if (a.M == 0) return DSK_OK;
+  const bool g = a.a_rows != nullptr;
+  if (a.b_tiled) {
+    if (swiglu) return g ? run_gemm_t<true, true, true>(a, st) : run_gemm_t<true, false, true>(a, st);
+    return g ? run_gemm_t<false, true, true>(a, st) : run_gemm_t<false, false, true>(a, st);
   }
-  if (gather) return launch_grouped_gemm<BM, BN, WM, WN, BK, ST, false, true>(a, st);
-  return launch_grouped_gemm<BM, BN, WM, WN, BK, ST, false, false>(a, st);
+  if (swiglu) return g ? run_gemm_t<true, true, false>(a, st) : run_gemm_t<true, false, false>(a, st);
+  return g ? run_gemm_t<false, true, false>(a, st) : run_gemm_t<false, false, false>(a, st);
 }
 
 int zero_uncovered_rows(uint16_t* C, int64_t ldc, int M, int N, const int32_t* offsets,

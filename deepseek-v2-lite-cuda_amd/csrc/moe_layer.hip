@@ -62,7 +62,8 @@ extern "C" size_t dsk_moe_fused_workspace_size(int num_tokens, int num_experts, 
 extern "C" int dsk_moe_fused_forward(const float* logits, const dsk_bf16* x, const dsk_bf16* w1,
                                      const dsk_bf16* w2, dsk_bf16* out, int num_tokens,
                                      int num_experts, int top_k, int n_shared_groups,
-                                     int hidden, int intermediate, int32_t* topk_idx_out,
+                                     int hidden, int intermediate, int weight_layout,
+                                     int32_t* topk_idx_out,
                                      float* topk_w_out, int32_t* expert_offsets_out,
                                      void* workspace, size_t workspace_bytes,
                                      void* const* stage_events, void* stream) {
@@ -77,6 +78,8 @@ extern "C" int dsk_moe_fused_forward(const float* logits, const dsk_bf16* x, con
   DSK_REQUIRE(T >= 0, DSK_ERR_INVALID_ARG, "moe_fused: num_tokens < 0");
   DSK_REQUIRE(H > 0 && H % 64 == 0 && I > 0 && I % 64 == 0, DSK_ERR_INVALID_ARG,
               "moe_fused: hidden and intermediate sizes must be multiples of 64");
+  DSK_REQUIRE(weight_layout == DSK_LAYOUT_ROW_MAJOR || weight_layout == DSK_LAYOUT_TILED,
+              DSK_ERR_INVALID_ARG, "moe_fused: unknown weight_layout");
   if (T == 0) return DSK_OK;
   DSK_REQUIRE(logits && x && w1 && w2 && out, DSK_ERR_NULL_PTR, "moe_fused: NULL pointer");
   DSK_REQUIRE(aligned16(x) && aligned16(w1) && aligned16(w2) && aligned16(out),
@@ -136,6 +139,8 @@ extern "C" int dsk_moe_fused_forward(const float* logits, const dsk_bf16* x, con
   g1.offsets = offsets; g1.G = G;
   g1.M = Stot; g1.N = I; g1.K = H;
   g1.up_row_offset = I;
+  g1.max_group_rows = T;  // a token routes to an expert at most once; shared groups hold T
+  g1.b_tiled = weight_layout == DSK_LAYOUT_TILED;
   if ((rc = run_gemm(g1, true, st))) return rc;
   if ((rc = mark(2))) return rc;
 
@@ -145,6 +150,8 @@ extern "C" int dsk_moe_fused_forward(const float* logits, const dsk_bf16* x, con
   g2.C = y; g2.ldc = H;
   g2.offsets = offsets; g2.G = G;
   g2.M = Stot; g2.N = H; g2.K = I;
+  g2.max_group_rows = T;
+  g2.b_tiled = weight_layout == DSK_LAYOUT_TILED;
   if ((rc = run_gemm(g2, false, st))) return rc;
   if ((rc = mark(3))) return rc;
 

@@ -18,7 +18,13 @@ from .ops import (  # noqa: F401
     rope,
     swiglu,
 )
-from .expert_prepack import pack_tensors, prepack_experts, prepack_with_shared  # noqa: F401
+from .expert_prepack import (  # noqa: F401
+    pack_tensors,
+    prepack_experts,
+    prepack_with_shared,
+    tile_weights,
+    untile_weights,
+)
 from .moe_fused import (  # noqa: F401
     FusedMoELayer,
     fused_moe_forward,
@@ -29,6 +35,7 @@ from .moe_fused import (  # noqa: F401
 __all__ = [
     "moe_routing", "moe_scan", "moe_dispatch", "moe_combine", "swiglu", "moe_gemm1",
     "moe_gemm1_swiglu", "moe_gemm2", "rms_norm", "kv_upproj", "linear", "rope",
-    "prepack_experts", "prepack_with_shared", "pack_tensors", "FusedMoELayer",
+    "prepack_experts", "prepack_with_shared", "pack_tensors", "tile_weights", "untile_weights",
+    "FusedMoELayer",
     "fused_moe_forward", "moe_fused_forward_logits", "route_dispatch_combine", "DskError",
 ]

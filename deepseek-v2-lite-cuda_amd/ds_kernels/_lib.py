@@ -44,8 +44,8 @@ SIGNATURES = {
     "dsk_rope_qk": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _P, _I64, _I64,
                          _P, _P, _I, _I, _I, _I, _I, _P]),
     "dsk_moe_fused_workspace_size": (_SZ, [_I, _I, _I, _I, _I, _I]),
-    "dsk_moe_fused_forward": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P,
-                                   _P, _SZ, _P, _P]),
+    "dsk_moe_fused_forward": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P,
+                                   _P, _P, _SZ, _P, _P]),
 }
 
 

@@ -4,6 +4,12 @@ Layouts consumed by the grouped GEMMs (nn.Linear [out, in] order, K-contiguous):
   packed_w1[g] = cat(gate_proj.weight, up_proj.weight)   [G, 2I, H]
   w2[g]        = down_proj.weight                          [G, H, I]
 
+tile_weights() rewrites either into the fragment-tiled layout the fused layer
+also accepts (DSK_LAYOUT_TILED in include/dsk.h): [G, N/32, K/16, 64, 8], one
+1 KB MFMA fragment (32 rows x 16 columns, lane l = row l % 32, columns
+8*(l // 32) .. +7) per [64, 8] slice, so a wave loads a fragment as 1 KB of
+consecutive bytes. It is a pure permutation of the same elements.
+
 prepack_with_shared() appends the shared expert (intermediate n_sh * I) as n_sh
 extra groups of width I: group E + j takes gate/up rows [j*I, (j+1)*I) and the
 matching down columns. Since down(silu(gate x) * up x) splits exactly over
@@ -62,6 +68,22 @@ def pack_tensors(gates: Sequence[torch.Tensor], ups: Sequence[torch.Tensor],
     return w1, w2, nsh
 
 
+def tile_weights(w: torch.Tensor) -> torch.Tensor:
+    """[G, N, K] row-major -> [G, N/32, K/16, 64, 8] fragment-tiled (same dtype/device)."""
+    G, N, K = w.shape
+    if N % 32 or K % 16:
+        raise ValueError(f"tile_weights: [{G}, {N}, {K}] needs N % 32 == 0 and K % 16 == 0")
+    return (w.reshape(G, N // 32, 32, K // 16, 2, 8).permute(0, 1, 3, 4, 2, 5)
+            .reshape(G, N // 32, K // 16, 64, 8).contiguous())
+
+
+def untile_weights(wt: torch.Tensor) -> torch.Tensor:
+    """Inverse of tile_weights: [G, N/32, K/16, 64, 8] -> [G, N, K]."""
+    G, NB, KS = wt.shape[:3]
+    return (wt.reshape(G, NB, KS, 2, 32, 8).permute(0, 1, 4, 2, 3, 5)
+            .reshape(G, NB * 32, KS * 16).contiguous())
+
+
 def prepack_experts(experts: List) -> Tuple[torch.Tensor, torch.Tensor]:
     """Reference-compatible packing: (packed_w1 [E,2I,H], w2 [E,H,I]) in bf16 on
     the experts' (CUDA) device."""
@@ -78,14 +100,18 @@ def prepack_experts(experts: List) -> Tuple[torch.Tensor, torch.Tensor]:
 
 
 def prepack_with_shared(experts: List, shared_expert=None,
-                        device: Optional[torch.device] = None
+                        device: Optional[torch.device] = None, tiled: bool = True
                         ) -> Tuple[torch.Tensor, torch.Tensor, int]:
     """Packing for the fused layer: routed experts then the shared expert split
-    into width-I groups. Returns (w1, w2, n_shared_groups)."""
+    into width-I groups, fragment-tiled unless tiled=False.
+    Returns (w1, w2, n_shared_groups)."""
     ws = [_weights(e) for e in experts]
     shared = _weights(shared_expert) if shared_expert is not None else None
-    return pack_tensors([w[0] for w in ws], [w[1] for w in ws], [w[2] for w in ws],
-                        device=device, shared=shared)
+    w1, w2, nsh = pack_tensors([w[0] for w in ws], [w[1] for w in ws], [w[2] for w in ws],
+                               device=device, shared=shared)
+    if tiled:
+        w1, w2 = tile_weights(w1), tile_weights(w2)
+    return w1, w2, nsh
 
 
 def verify_prepack(experts: List) -> bool:

@@ -33,7 +33,9 @@ def moe_fused_forward_logits(logits: torch.Tensor, hidden_states: torch.Tensor,
                              workspace: Optional[torch.Tensor] = None):
     """Whole MoE layer from precomputed fp32 gate logits [T, E].
 
-    w1: [E + n_shared_groups, 2I, H] bf16, w2: [E + n_shared_groups, H, I] bf16.
+    w1: [E + n_shared_groups, 2I, H] bf16, w2: [E + n_shared_groups, H, I] bf16,
+    row-major, or both fragment-tiled by expert_prepack.tile_weights
+    ([G, 2I/32, H/16, 64, 8] and [G, H/32, I/16, 64, 8]).
     Returns out [T, H] bf16 (and (topk_idx, topk_w, expert_offsets) if asked).
     stage_events: optional ctypes array of 5 hipEvent_t handles recorded at the
     stage boundaries (instrumentation for benchmarks). workspace: optional
@@ -41,13 +43,21 @@ def moe_fused_forward_logits(logits: torch.Tensor, hidden_states: torch.Tensor,
     op = "moe_fused_forward"
     T, H = hidden_states.shape
     E = logits.shape[1] if num_experts is None else num_experts
-    G, N2, Hw = w1.shape
+    tiled = w1.dim() == 5
+    if tiled:
+        if w2.dim() != 5 or tuple(w1.shape[3:]) != (64, 8) or tuple(w2.shape[3:]) != (64, 8):
+            raise RuntimeError(f"{op}: tiled w1/w2 must both be [G, N/32, K/16, 64, 8]")
+        G, N2, Hw = w1.shape[0], w1.shape[1] * 32, w1.shape[2] * 16
+        w2_shape = (w2.shape[0], w2.shape[1] * 32, w2.shape[2] * 16)
+    else:
+        G, N2, Hw = w1.shape
+        w2_shape = tuple(w2.shape)
     I = N2 // 2
     for t, n, dt in ((logits, "logits", torch.float32), (hidden_states, "hidden_states", torch.bfloat16),
                      (w1, "w1", torch.bfloat16), (w2, "w2", torch.bfloat16)):
         if not (t.is_cuda and t.is_contiguous() and t.dtype == dt):
             raise RuntimeError(f"{op}: {n} must be a contiguous CUDA {dt} tensor")
-    if logits.shape != (T, E) or G != E + n_shared_groups or Hw != H or tuple(w2.shape) != (G, H, I):
+    if logits.shape != (T, E) or G != E + n_shared_groups or Hw != H or w2_shape != (G, H, I):
         raise RuntimeError(f"{op}: inconsistent shapes logits={tuple(logits.shape)} "
                            f"x={tuple(hidden_states.shape)} w1={tuple(w1.shape)} w2={tuple(w2.shape)}")
     dev = hidden_states.device
@@ -67,7 +77,7 @@ def moe_fused_forward_logits(logits: torch.Tensor, hidden_states: torch.Tensor,
     with torch.cuda.device(dev):
         check(lib.dsk_moe_fused_forward(
             logits.data_ptr(), hidden_states.data_ptr(), w1.data_ptr(), w2.data_ptr(),
-            out.data_ptr(), T, E, top_k, n_shared_groups, H, I,
+            out.data_ptr(), T, E, top_k, n_shared_groups, H, I, 1 if tiled else 0,
             idx.data_ptr() if idx is not None else None,
             w.data_ptr() if w is not None else None,
             offs.data_ptr() if offs is not None else None,

@@ -39,6 +39,10 @@ enum {
   DSK_ERR_WORKSPACE = 5      /* workspace too small                        */
 };
 
+/* Expert weight layouts accepted by dsk_moe_fused_forward. */
+#define DSK_LAYOUT_ROW_MAJOR 0
+#define DSK_LAYOUT_TILED 1
+
 /* Limits mirrored from the reference routing kernel (routing.cu:32-33). */
 #define DSK_MAX_EXPERTS 64
 #define DSK_MAX_TOP_K 6
@@ -187,7 +191,16 @@ int dsk_rope_qk(const dsk_bf16* q, int64_t qsb, int64_t qsh, int64_t qss,
  *   deterministic combine (+ shared expert), with no host synchronisation.
  * logits: fp32 [T, E] (gate GEMM output, as moe_fused.py:131 computes it);
  * x: bf16 [T, H]; w1: bf16 [G, 2I, H] and w2: bf16 [G, H, I] where
- * G = E + n_shared_groups. Groups E.. are the shared expert split into
+ * G = E + n_shared_groups, stored as selected by weight_layout:
+ *   DSK_LAYOUT_ROW_MAJOR  nn.Linear order, each group [N, K] K-contiguous
+ *                         (the reference prepack, expert_prepack.py:105-130);
+ *   DSK_LAYOUT_TILED      MFMA-fragment order: a group's [N, K] matrix is cut
+ *                         into 32-row x 16-column fragments, fragment (rb, ks)
+ *                         at element (rb * K/16 + ks) * 512, and inside it
+ *                         element (r, k) at ((k / 8) * 32 + r) * 8 + k % 8.
+ *                         Each 1 KB fragment is then one coalesced 64-lane
+ *                         load (decode streams the weights at full HBM rate).
+ * Groups E.. are the shared expert split into
  * n_shared_groups slices of width I (every token routes to them with weight
  * 1.0). out: bf16 [T, H]. The replaced reference caller is
  * _route_dispatch_combine (moe_fused.py:118-154), which omits shared experts.
@@ -202,7 +215,7 @@ int dsk_moe_fused_forward(const float* logits, const dsk_bf16* x,
                           const dsk_bf16* w1, const dsk_bf16* w2,
                           dsk_bf16* out, int num_tokens, int num_experts,
                           int top_k, int n_shared_groups, int hidden,
-                          int intermediate, int32_t* topk_idx_out,
+                          int intermediate, int weight_layout, int32_t* topk_idx_out,
                           float* topk_w_out, int32_t* expert_offsets_out,
                           void* workspace, size_t workspace_bytes,
                           void* const* stage_events, void* stream);

@@ -36,7 +36,7 @@ def test_every_declared_symbol_is_exported(dsk):
 
 
 def test_abi_version(dsk):
-    assert dsk.lib.dsk_abi_version() == 1
+    assert dsk.lib.dsk_abi_version() == 2
 
 
 def _err(dsk):
@@ -89,12 +89,15 @@ def test_fused_validation_and_workspace_sizes(dsk):
         (4096 * 8) * (2048 + 1408) * 2
     assert lib.dsk_moe_dispatch_workspace_size(100, 64, 6) >= 2 * 100 * 6 * 4
     assert lib.dsk_moe_combine_workspace_size(600, 100) >= (2 * 101 + 2 * 600) * 4
-    rc = lib.dsk_moe_fused_forward(None, None, None, None, None, 4, 64, 6, 2, 2048, 1400, None,
-                                   None, None, None, 0, None, None)
+    rc = lib.dsk_moe_fused_forward(None, None, None, None, None, 4, 64, 6, 2, 2048, 1400, 0,
+                                   None, None, None, None, 0, None, None)
     assert rc == 1
-    rc = lib.dsk_moe_fused_forward(16, 16, 16, 16, 16, 4, 64, 6, 2, 2048, 1408, None, None, None,
-                                   None, 0, None, None)
+    rc = lib.dsk_moe_fused_forward(16, 16, 16, 16, 16, 4, 64, 6, 2, 2048, 1408, 0, None, None,
+                                   None, None, 0, None, None)
     assert rc == 5 and "workspace" in _err(dsk)
+    rc = lib.dsk_moe_fused_forward(16, 16, 16, 16, 16, 4, 64, 6, 2, 2048, 1408, 7, None, None,
+                                   None, None, 0, None, None)
+    assert rc == 1 and "weight_layout" in _err(dsk)
 
 
 def test_python_ops_reject_cpu_tensors(dsk):

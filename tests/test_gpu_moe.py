@@ -187,6 +187,26 @@ def test_gemm_skewed_groups_and_uncovered_rows(dsk):
     assert torch.all(out[int(off[-1]):] == 0)
 
 
+@pytest.mark.parametrize("counts", [[64], [33, 0, 31], [1, 0, 0, 17, 32, 0, 14], [0, 0, 5]])
+def test_gemm_small_groups(dsk, counts):
+    """At most 64 slots in total: the small-group (decode) kernel, with 1 and 2
+    token blocks, empty groups, and rows past the last group left at zero."""
+    E = len(counts)
+    off = om.scan(np.array(counts, np.int32))
+    S = int(off[-1]) + 2
+    offd = torch.from_numpy(off).to(DEV)
+    a, w = _gemm_inputs(S, 2816, 2048, E, 300 + S)
+    ref1 = om.grouped_linear(np32(a), np32(w), off)
+    out = dsk.moe_gemm1(a.to(DEV), w.to(DEV), offd)
+    assert max_rel_err(np32(out), ref1) <= BF16_TOL
+    assert torch.all(out[int(off[-1]):] == 0)
+    sw = dsk.moe_gemm1_swiglu(a.to(DEV), w.to(DEV), offd)
+    assert max_rel_err(np32(sw), om.swiglu(ref1)) <= BF16_TOL
+    h, w2 = _gemm_inputs(S, 2048, 1408, E, 400 + S)
+    out2 = dsk.moe_gemm2(h.to(DEV), w2.to(DEV), offd)
+    assert max_rel_err(np32(out2), om.grouped_linear(np32(h), np32(w2), off)) <= BF16_TOL
+
+
 def test_gemm_zero_slots(dsk):
     out = dsk.moe_gemm1(torch.empty(0, 2048, dtype=torch.bfloat16, device=DEV),
                         torch.zeros(64, 2816, 2048, dtype=torch.bfloat16, device=DEV),
@@ -227,12 +247,22 @@ def full_layer(dsk):
     return W, w1, w2, nsh, Wn
 
 
+@pytest.fixture(scope="module")
+def tiled_layer(dsk, full_layer):
+    W, w1, w2, nsh, Wn = full_layer
+    return dsk.tile_weights(w1), dsk.tile_weights(w2)
+
+
+@pytest.mark.parametrize("layout", ["row_major", "tiled"])
 @pytest.mark.parametrize("T,bias", [(64, False), (4096, False), (1, True), (4, True),
-                                    (16, True), (64, True)])
-def test_fused_layer_matches_oracle(dsk, full_layer, T, bias):
-    """Configs 0/1 (near-uniform routing) and 2 (Zipf-biased router), bf16."""
+                                    (16, True), (64, True), (100, True)])
+def test_fused_layer_matches_oracle(dsk, full_layer, tiled_layer, T, bias, layout):
+    """Configs 0/1 (near-uniform routing) and 2 (Zipf-biased router), bf16, with
+    the expert weights row-major or fragment-tiled."""
     from ds_kernels import synthetic as syn
     W, w1, w2, nsh, Wn = full_layer
+    if layout == "tiled":
+        w1, w2 = tiled_layer
     x = syn.tokens(T).to(torch.bfloat16)
     xd = x.to(DEV)
     logits = F.linear(xd.float(), W.wg.to(torch.bfloat16).float().to(DEV))
