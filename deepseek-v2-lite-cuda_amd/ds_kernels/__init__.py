@@ -11,6 +11,7 @@ from .ops import (  # noqa: F401
     moe_dispatch,
     moe_gemm1,
     moe_gemm1_swiglu,
+    moe_gate,
     moe_gemm2,
     moe_routing,
     moe_scan,
@@ -33,7 +34,7 @@ from .moe_fused import (  # noqa: F401
 )
 
 __all__ = [
-    "moe_routing", "moe_scan", "moe_dispatch", "moe_combine", "swiglu", "moe_gemm1",
+    "moe_gate", "moe_routing", "moe_scan", "moe_dispatch", "moe_combine", "swiglu", "moe_gemm1",
     "moe_gemm1_swiglu", "moe_gemm2", "rms_norm", "kv_upproj", "linear", "rope",
     "prepack_experts", "prepack_with_shared", "pack_tensors", "tile_weights", "untile_weights",
     "FusedMoELayer",

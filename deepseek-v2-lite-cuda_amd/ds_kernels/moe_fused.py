@@ -10,7 +10,10 @@ Two levels are offered, as in the reference:
     route -> permutation -> GEMM1+SwiGLU -> GEMM2 -> combine with the shared
     expert folded into the grouped GEMMs, and no host synchronisation.
 
-The gate logits stay a torch fp32 linear, as at moe_fused.py:131.
+Gate logits: with a bf16 gate weight they come from the library's gate kernel
+(ops.moe_gate: bf16 products, fp32 accumulation, as F.linear(x.float(),
+w.float()) at moe_fused.py:131 up to fp32 summation order); with an fp32 gate
+weight they stay the torch fp32 linear.
 """
 from __future__ import annotations
 
@@ -87,6 +90,16 @@ def moe_fused_forward_logits(logits: torch.Tensor, hidden_states: torch.Tensor,
     return out
 
 
+def gate_logits(hidden_states: torch.Tensor, gate_weight: torch.Tensor,
+                bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """fp32 router logits [T, E]: the gate kernel for a bf16 gate weight, else
+    torch's fp32 linear (the reference's own formula)."""
+    if gate_weight.dtype == torch.bfloat16 and hidden_states.dtype == torch.bfloat16:
+        return ops.moe_gate(hidden_states, gate_weight, bias)
+    logits = F.linear(hidden_states.float(), gate_weight.float(), None)
+    return logits + bias if bias is not None else logits
+
+
 def route_dispatch_combine(hidden_states: torch.Tensor, gate_weight: torch.Tensor,
                            packed_w1: torch.Tensor, w2: torch.Tensor, top_k: int,
                            fuse_swiglu: bool = False) -> torch.Tensor:
@@ -129,7 +142,7 @@ class FusedMoELayer(nn.Module):
         assert hidden_states.dtype == torch.bfloat16, "hidden_states must be BF16."
         orig = hidden_states.shape
         x = hidden_states.reshape(-1, orig[-1]).contiguous()
-        logits = F.linear(x.float(), self.gate_weight.float(), None)
+        logits = gate_logits(x, self.gate_weight)
         out = moe_fused_forward_logits(logits, x, self.w1, self.w2, self.top_k,
                                        self.n_shared_groups, self.num_experts)
         return out.view(orig)
@@ -152,6 +165,6 @@ def fused_moe_forward(hidden_states: torch.Tensor, gate_weight: torch.Tensor, ex
         if key not in _WEIGHT_CACHE:
             _WEIGHT_CACHE[key] = prepack_experts(experts)
         packed_w1, w2 = _WEIGHT_CACHE[key]
-    logits = F.linear(hidden_states.float(), gate_weight.float(), None)
+    logits = gate_logits(hidden_states.contiguous(), gate_weight)
     return moe_fused_forward_logits(logits, hidden_states.contiguous(), packed_w1, w2, top_k, 0,
                                     packed_w1.shape[0])

@@ -38,6 +38,36 @@ def _ws(nbytes: int, device: torch.device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
 
 
+# -------------------------------------------------------------- gate logits --
+def moe_gate(x: torch.Tensor, weight: torch.Tensor,
+             bias: "torch.Tensor | None" = None) -> torch.Tensor:
+    """Router logits fp32 [T, E] = x @ weight^T (+ bias), bf16 in, fp32 accumulation.
+
+    Replaces F.linear(x.float(), weight.float()) (moe_fused.py:131, moe.py:35-37);
+    bias (fp32 [E]) is an optional per-expert routing bias added to the logits."""
+    op = "moe_gate"
+    _req(x.is_cuda and weight.is_cuda, f"{op}: x and weight must be CUDA tensors.")
+    _dtype(x, torch.bfloat16, "x", op)
+    _dtype(weight, torch.bfloat16, "weight", op)
+    _req(x.dim() == 2 and x.stride(1) == 1, f"{op}: x must be [tokens, hidden] with unit column stride.")
+    _cuda_contig(weight, "weight", op)
+    T, H = x.shape
+    E = weight.shape[0]
+    _req(weight.dim() == 2 and weight.shape[1] == H, f"{op}: weight must be [experts, {H}].")
+    _req(E <= MAX_EXPERTS, "num_experts must not exceed 64.")
+    if bias is not None:
+        _cuda_contig(bias, "bias", op)
+        _dtype(bias, torch.float32, "bias", op)
+        _req(tuple(bias.shape) == (E,), f"{op}: bias must be [{E}].")
+    dev = x.device
+    logits = torch.empty((T, E), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        check(lib.dsk_moe_gate_logits(x.data_ptr(), x.stride(0), weight.data_ptr(),
+                                      bias.data_ptr() if bias is not None else None,
+                                      logits.data_ptr(), E, T, E, H, stream_handle(dev)), op)
+    return logits
+
+
 # ----------------------------------------------------------------- routing --
 def moe_routing(logits: torch.Tensor, top_k: int = 6) -> List[torch.Tensor]:
     """Fused softmax + top-k routing (routing.cu:266-301).

@@ -52,6 +52,20 @@ const char* dsk_last_error(void);
 /* ABI version of this library (bumped on any signature change). */
 int dsk_abi_version(void);
 
+/* ------------------------------------------------------------ gate logits --
+ * logits[t, e] = sum_k x[t, k] * gate_weight[e, k] (+ bias[e] if bias is not
+ * NULL), bf16 inputs, fp32 accumulation and output. Replaces the fp32
+ * F.linear(x.float(), gate.weight.float()) of the reference orchestrator
+ * (moe_fused.py:131) and of MoEGate.forward (moe.py:35-37); same products,
+ * summation order fixed by this kernel (results differ from torch's only by
+ * fp32 rounding). The optional bias is a per-expert routing bias added to the
+ * logits (the Zipf-skewed router of BASELINE config 2 is such a bias).
+ * x: bf16 [T, H] row stride ld_x; gate_weight: bf16 [E, H] contiguous;
+ * logits: fp32 [T, E] row stride ld_logits. E <= 64, H % 16 == 0. */
+int dsk_moe_gate_logits(const dsk_bf16* x, int64_t ld_x, const dsk_bf16* gate_weight,
+                        const float* bias, float* logits, int64_t ld_logits,
+                        int num_tokens, int num_experts, int hidden, void* stream);
+
 /* ---------------------------------------------------------------- routing --
  * Softmax over E expert logits + top-K (ties -> lower expert index, emitted in
  * descending-weight order) + per-expert counts.

@@ -83,6 +83,20 @@ def test_norm_rope_validation(dsk):
     assert rc == 1
 
 
+def test_gate_validation(dsk):
+    lib = dsk.lib
+    rc = lib.dsk_moe_gate_logits(16, 2048, 16, None, 16, 65, 4, 65, 2048, None)
+    assert rc == 1 and "64" in _err(dsk)
+    rc = lib.dsk_moe_gate_logits(16, 2048, 16, None, 16, 64, 4, 64, 2040, None)
+    assert rc == 1 and "16" in _err(dsk)
+    rc = lib.dsk_moe_gate_logits(None, 2048, 16, None, 16, 64, 4, 64, 2048, None)
+    assert rc == 2
+    rc = lib.dsk_moe_gate_logits(16, 2052, 16, None, 16, 64, 4, 64, 2048, None)
+    assert rc == 3
+    rc = lib.dsk_moe_gate_logits(16, 2040, 16, None, 16, 64, 4, 64, 2048, None)
+    assert rc == 1 and "stride" in _err(dsk)
+
+
 def test_fused_validation_and_workspace_sizes(dsk):
     lib = dsk.lib
     assert lib.dsk_moe_fused_workspace_size(4096, 64, 6, 2, 2048, 1408) > \

@@ -26,6 +26,38 @@ def dsk():
     return ds_kernels
 
 
+# -------------------------------------------------------------- gate logits --
+@pytest.mark.parametrize("T,E,H,bias", [(1, 64, 2048, True), (16, 64, 2048, True),
+                                        (64, 64, 2048, False), (100, 40, 512, True),
+                                        (4096, 64, 2048, False)])
+def test_gate_logits_match_fp64(dsk, T, E, H, bias):
+    """fp32 logits of bf16 x and gate weight vs the same dot products in fp64
+    (the products are exact; only the fp32 summation differs): <= 1e-5."""
+    g = torch.Generator().manual_seed(T + E)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    wg = (torch.randn(E, H, generator=g) * 0.02).to(torch.bfloat16)
+    b = (torch.randn(E, generator=g)).float() if bias else None
+    xd = x.contiguous().to(DEV)
+    out = dsk.moe_gate(xd, wg.to(DEV), b.to(DEV) if b is not None else None)
+    ref = x.double().numpy() @ wg.double().numpy().T
+    if b is not None:
+        ref = ref + b.double().numpy()
+    assert out.shape == (T, E) and out.dtype == torch.float32
+    err = np.abs(out.cpu().double().numpy() - ref).max() / np.abs(ref).max()
+    assert err <= F32_TOL, err
+    assert torch.equal(out, dsk.moe_gate(xd, wg.to(DEV), b.to(DEV) if b is not None else None))
+
+
+def test_gate_logits_strided_rows(dsk):
+    g = torch.Generator().manual_seed(5)
+    big = torch.randn(48, 2048 + 256, generator=g).to(torch.bfloat16).to(DEV)
+    x = big[:, 128:128 + 2048]          # row stride 2304
+    wg = (torch.randn(64, 2048, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    out = dsk.moe_gate(x, wg)
+    ref = x.double().cpu().numpy() @ wg.double().cpu().numpy().T
+    assert np.abs(out.cpu().double().numpy() - ref).max() / np.abs(ref).max() <= F32_TOL
+
+
 # ------------------------------------------------------------------ routing --
 @pytest.mark.parametrize("T,E,K", [(1, 64, 6), (32, 64, 6), (128, 64, 6), (4096, 64, 6),
                                    (100, 16, 4), (65, 64, 1)])
