@@ -2,7 +2,7 @@
 """Benchmark of the fused DeepSeek-V2-Lite MoE layer on one MI355X.
 
 Headline (value): prefill MoE layer tokens/s at T=4096, bf16:
-one step = gate logits (library gate kernel: bf16 products, fp32 accumulation) + the fused layer
+one step = dsk_moe_layer_forward: gate logits (bf16 products, fp32 accumulation) + the fused layer
 (route -> permutation -> grouped GEMM1+SwiGLU -> grouped GEMM2 -> combine, the
 2 shared experts included) over 4096 resident tokens.
 
@@ -71,17 +71,15 @@ class HipEvents:
 def bench_prefill(dsk, syn, torch, F, W, packed, T, steps, warmup, ev):
     w1, w2, nsh = packed
     dev = w1.device
-    wg = W.wg.to(torch.bfloat16).to(dev)
+    wg = dsk.tile_weights(W.wg.to(torch.bfloat16)[None])[0].to(dev)   # fragment-tiled gate
     x = syn.tokens(T).to(torch.bfloat16).to(dev)
     H, I = 2048, 1408
-    ws = torch.empty(dsk.lib.dsk_moe_fused_workspace_size(T, 64, 6, nsh, H, I),
+    ws = torch.empty(dsk.lib.dsk_moe_layer_workspace_size(T, 64, 6, nsh, H, I),
                      dtype=torch.uint8, device=dev)
     events = [ev.create(5) for _ in range(steps)]
 
     def step(e=None):
-        logits = dsk.moe_gate(x, wg)
-        return dsk.moe_fused_forward_logits(logits, x, w1, w2, 6, nsh, 64, workspace=ws,
-                                            stage_events=e)
+        return dsk.moe_layer_forward(x, wg, w1, w2, 6, nsh, workspace=ws, stage_events=e)
 
     for _ in range(warmup):
         step()
@@ -97,7 +95,7 @@ def bench_prefill(dsk, syn, torch, F, W, packed, T, steps, warmup, ev):
     mean = lambda v: sum(v) / len(v)  # noqa: E731
     return {
         "ms_per_step": elapsed * 1e3 / steps,
-        "route_ms": mean([s[0] for s in stage]),
+        "gate_route_ms": mean([s[0] for s in stage]),
         "gemm1_ms": mean([s[1] for s in stage]),
         "gemm2_ms": mean([s[2] for s in stage]),
         "combine_ms": mean([s[3] for s in stage]),
@@ -108,21 +106,19 @@ def bench_prefill(dsk, syn, torch, F, W, packed, T, steps, warmup, ev):
 def bench_decode(dsk, syn, torch, F, W, packed, T, steps, ev, copies):
     w1, w2, nsh = packed
     dev = w1.device
-    wg = W.wg.to(torch.bfloat16).to(dev)
+    wg = dsk.tile_weights(W.wg.to(torch.bfloat16)[None])[0].to(dev)   # fragment-tiled gate
     bias = syn.zipf_router_bias().to(dev)
     x = syn.tokens(T).to(torch.bfloat16).to(dev)
     H, I = 2048, 1408
-    ws = torch.empty(dsk.lib.dsk_moe_fused_workspace_size(T, 64, 6, nsh, H, I),
+    ws = torch.empty(dsk.lib.dsk_moe_layer_workspace_size(T, 64, 6, nsh, H, I),
                      dtype=torch.uint8, device=dev)
 
     def step(c):
-        logits = dsk.moe_gate(x, wg, bias)
-        return dsk.moe_fused_forward_logits(logits, x, copies[c][0], copies[c][1], 6, nsh, 64,
-                                            workspace=ws)
+        return dsk.moe_layer_forward(x, wg, copies[c][0], copies[c][1], 6, nsh, gate_bias=bias,
+                                     workspace=ws)
 
-    logits = dsk.moe_gate(x, wg, bias)
-    _, (idx, _, off) = dsk.moe_fused_forward_logits(logits, x, w1, w2, 6, nsh, 64,
-                                                    return_routing=True)
+    _, (idx, _, off) = dsk.moe_layer_forward(x, wg, w1, w2, 6, nsh, gate_bias=bias,
+                                             return_routing=True)
     counts = (off[1:] - off[:-1]).cpu()
     e_active = int((counts > 0).sum())
     for i in range(5):
@@ -307,7 +303,7 @@ def main():
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": ach_g1 / PEAK_BF16_TFLOPS, "traffic": traffic,
                      "flops_per_launch": flops_g1, "mean_launch_ms": pre["gemm1_ms"]},
-        "stages_ms": {k: pre[k] for k in ("route_ms", "gemm1_ms", "gemm2_ms", "combine_ms")},
+        "stages_ms": {k: pre[k] for k in ("gate_route_ms", "gemm1_ms", "gemm2_ms", "combine_ms")},
         "gemm2": {"achieved_tflops": ach_g2, "frac": ach_g2 / PEAK_BF16_TFLOPS},
         "gemms_combined": {"achieved_tflops": ach_both, "frac": ach_both / PEAK_BF16_TFLOPS},
     }

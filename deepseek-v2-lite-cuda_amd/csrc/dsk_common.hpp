@@ -81,6 +81,36 @@ __device__ __forceinline__ float wave_sum(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Reductions over each 16-lane row (quad swaps, then the half-row and row
+// mirrors): every lane of the row ends with the row's result. Each step pairs
+// lane i with a partner p(i) that pairs back with i, so both compute the same
+// op(v_i, v_p) and the sums are bitwise equal on all 16 lanes.
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f32<0xB1>(v, v));
+  v = fmaxf(v, dpp_f32<0x4E>(v, v));
+  v = fmaxf(v, dpp_f32<0x141>(v, v));
+  v = fmaxf(v, dpp_f32<0x140>(v, v));
+  return v;
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f32<0xB1>(0.f, v);
+  v += dpp_f32<0x4E>(0.f, v);
+  v += dpp_f32<0x141>(0.f, v);
+  v += dpp_f32<0x140>(0.f, v);
+  return v;
+}
+template <int kCtrl>
+__device__ __forceinline__ int dpp_i32(int v) {
+  return __builtin_amdgcn_update_dpp(v, v, kCtrl, 0xf, 0xf, false);
+}
+__device__ __forceinline__ int row16_min(int v) {
+  v = min(v, dpp_i32<0xB1>(v));
+  v = min(v, dpp_i32<0x4E>(v));
+  v = min(v, dpp_i32<0x141>(v));
+  v = min(v, dpp_i32<0x140>(v));
+  return v;
+}
+
 // Inclusive prefix sum of an int over the 64 lanes (Hillis-Steele on shuffles;
 // only used by the small scan kernels).
 __device__ __forceinline__ int wave_inclusive_scan(int v) {

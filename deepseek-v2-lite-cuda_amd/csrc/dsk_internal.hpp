@@ -28,9 +28,17 @@ struct GemmArgs {
 
 int run_gemm(const GemmArgs& a, bool swiglu, hipStream_t st);
 
-int launch_route(const float* logits, int64_t ld, int T, int E, int K, int32_t* idx, float* w,
+// Router logits for routing = sum over n_parts partial-sum planes
+// (logits + s * part_stride, s < n_parts, fixed order) + bias[e] if given.
+int launch_route(const float* logits, int64_t ld, int n_parts, int64_t part_stride,
+                 const float* bias, int T, int E, int K, int32_t* idx, float* w,
                  int32_t* blk_hist, int32_t* local_rank, int32_t* counts, int32_t* offsets,
                  int32_t* token_map, int32_t* slot_of, int n_extra_groups, hipStream_t st);
+// Partial gate sums: parts[s][t][e] = sum over the s-th of n_parts K slices of
+// x[t, k] * wg[e, k] (fp32), for the route kernel to add up.
+int gate_parts_count(int T, int E, int H);
+int launch_gate_parts(const uint16_t* x, int64_t ld_x, const uint16_t* wg, bool tiled,
+                      float* parts, int T, int E, int H, int n_parts, hipStream_t st);
 int launch_scan(const int32_t* hist, int nblk, int E, int32_t* counts, int32_t* offsets,
                 int32_t* blk_base, int n_extra_groups, int extra_rows, hipStream_t st);
 int launch_permute(const int32_t* idx, const float* w, int T, int K, int E,

@@ -22,6 +22,7 @@ namespace dsk {
 constexpr int kGateWaves = 16;
 constexpr int kGateChunk = 8;  // K steps (of 16) loaded before the MFMAs
 
+template <bool TILED>
 __global__ __launch_bounds__(64 * kGateWaves) void gate_logits_kernel(
     const uint16_t* __restrict__ x, int64_t ld_x, const uint16_t* __restrict__ wg,
     const float* __restrict__ bias, float* __restrict__ logits, int64_t ld_out, int T, int E,
@@ -34,9 +35,14 @@ __global__ __launch_bounds__(64 * kGateWaves) void gate_logits_kernel(
   // weights are MFMA operand A (output rows = experts), tokens operand B
   const int e = min(e0 + r32, E - 1);
   const int t = min(t0 + r32, T - 1);
-  const uint16_t* wrow = wg + (int64_t)e * H + 8 * h;
-  const uint16_t* xrow = x + (int64_t)t * ld_x + 8 * h;
   const int ksteps = H / 16;
+  // row-major weight: row e, 16 elements per K step (each load touches 32
+  // rows); fragment-tiled weight: fragment (expert block, K step) is 512
+  // consecutive elements, lane-ordered (each load reads 1 KB contiguous)
+  const uint16_t* wrow = TILED ? wg + ((int64_t)blockIdx.y * ksteps) * 512 + lane * 8
+                               : wg + (int64_t)e * H + 8 * h;
+  constexpr int kWStep = TILED ? 512 : 16;
+  const uint16_t* xrow = x + (int64_t)t * ld_x + 8 * h;
   const int s_beg = wave * ksteps / kGateWaves;
   const int s_end = (wave + 1) * ksteps / kGateWaves;
 
@@ -48,7 +54,7 @@ __global__ __launch_bounds__(64 * kGateWaves) void gate_logits_kernel(
 #pragma unroll
     for (int u = 0; u < kGateChunk; ++u) {
       const int s = min(s0 + u, s_end - 1);  // past the slice: reload, unused
-      wf[u] = *reinterpret_cast<const bf16x8_t*>(wrow + 16 * s);
+      wf[u] = *reinterpret_cast<const bf16x8_t*>(wrow + kWStep * s);
       tf[u] = *reinterpret_cast<const bf16x8_t*>(xrow + 16 * s);
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -87,14 +93,87 @@ __global__ __launch_bounds__(64 * kGateWaves) void gate_logits_kernel(
   }
 }
 
+// Partial gate sums for the fused layer: one wave per (32 tokens, 32 experts,
+// K slice), no LDS and no reduction here; the route kernel adds the n_parts
+// planes in a fixed order while it loads the logits. Splitting K over many
+// single-wave workgroups is what spreads the 256 KB of gate weight over the
+// CUs at decode sizes, where there are only one or two token blocks.
+template <bool TILED>
+__global__ __launch_bounds__(64) void gate_parts_kernel(
+    const uint16_t* __restrict__ x, int64_t ld_x, const uint16_t* __restrict__ wg,
+    float* __restrict__ parts, int T, int E, int H) {
+  const int lane = threadIdx.x;
+  const int t0 = blockIdx.x * 32, e0 = blockIdx.y * 32;
+  const int r32 = lane & 31, h = lane >> 5;
+  const int e = min(e0 + r32, E - 1);
+  const int t = min(t0 + r32, T - 1);
+  const int ksteps = H / 16;
+  const int s_beg = blockIdx.z * ksteps / gridDim.z;
+  const int s_end = (blockIdx.z + 1) * ksteps / gridDim.z;
+  const uint16_t* wrow = TILED ? wg + ((int64_t)blockIdx.y * ksteps) * 512 + lane * 8
+                               : wg + (int64_t)e * H + 8 * h;
+  constexpr int kWStep = TILED ? 512 : 16;
+  const uint16_t* xrow = x + (int64_t)t * ld_x + 8 * h;
+  floatx16_t acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+  for (int s0 = s_beg; s0 < s_end; s0 += kGateChunk) {
+    bf16x8_t wf[kGateChunk], tf[kGateChunk];
+#pragma unroll
+    for (int u = 0; u < kGateChunk; ++u) {
+      const int s = min(s0 + u, s_end - 1);
+      wf[u] = *reinterpret_cast<const bf16x8_t*>(wrow + kWStep * s);
+      tf[u] = *reinterpret_cast<const bf16x8_t*>(xrow + 16 * s);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < kGateChunk; ++u) {
+      if (s0 + u >= s_end) tf[u] = bf16x8_t{};
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[u], tf[u], acc, 0, 0, 0);
+    }
+  }
+  const int tok = t0 + r32;
+  if (tok >= T) return;
+  float* orow = parts + ((int64_t)blockIdx.z * T + tok) * E;
+#pragma unroll
+  for (int qg = 0; qg < 4; ++qg) {
+    const int eb = e0 + 8 * qg + 4 * h;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      if (eb + c < E) orow[eb + c] = acc[4 * qg + c];
+  }
+}
+
+// K slices for the partial gate sums: enough single-wave workgroups to reach
+// most CUs at decode sizes, one plane when the token blocks already do.
+int gate_parts_count(int T, int E, int H) {
+  const int blocks = ((T + 31) / 32) * ((E + 31) / 32);
+  int n = 512 / blocks;
+  n = n < 1 ? 1 : (n > 16 ? 16 : n);  // the route kernel adds at most 16 planes
+  return n > H / 16 ? H / 16 : n;
+}
+
+int launch_gate_parts(const uint16_t* x, int64_t ld_x, const uint16_t* wg, bool tiled,
+                      float* parts, int T, int E, int H, int n_parts, hipStream_t st) {
+  dim3 grid((T + 31) / 32, (E + 31) / 32, n_parts);
+  auto kern = tiled ? gate_parts_kernel<true> : gate_parts_kernel<false>;
+  hipLaunchKernelGGL(kern, grid, dim3(64), 0, st, x, ld_x, wg, parts, T, E, H);
+  return check_launch("gate_parts_kernel");
+}
+
 }  // namespace dsk
 
 using namespace dsk;
 
 extern "C" int dsk_moe_gate_logits(const dsk_bf16* x, int64_t ld_x, const dsk_bf16* gate_weight,
                                    const float* bias, float* logits, int64_t ld_logits,
-                                   int num_tokens, int num_experts, int hidden, void* stream) {
+                                   int num_tokens, int num_experts, int hidden,
+                                   int weight_layout, void* stream) {
   const int T = num_tokens, E = num_experts, H = hidden;
+  DSK_REQUIRE(weight_layout == DSK_LAYOUT_ROW_MAJOR ||
+                  (weight_layout == DSK_LAYOUT_TILED && E % 32 == 0),
+              DSK_ERR_INVALID_ARG,
+              "moe_gate: weight_layout must be row-major, or tiled with num_experts % 32 == 0");
   DSK_REQUIRE(T >= 0 && E >= 1 && E <= DSK_MAX_EXPERTS, DSK_ERR_INVALID_ARG,
               "moe_gate: num_experts must be in [1, 64] and num_tokens >= 0");
   DSK_REQUIRE(H > 0 && H % 16 == 0, DSK_ERR_INVALID_ARG,
@@ -106,7 +185,9 @@ extern "C" int dsk_moe_gate_logits(const dsk_bf16* x, int64_t ld_x, const dsk_bf
   DSK_REQUIRE(ld_x >= H && ld_logits >= E, DSK_ERR_INVALID_ARG,
               "moe_gate: row stride smaller than the row");
   dim3 grid((T + 31) / 32, (E + 31) / 32);
-  hipLaunchKernelGGL(gate_logits_kernel, grid, dim3(64 * kGateWaves), 0, as_stream(stream),
+  auto kern = weight_layout == DSK_LAYOUT_TILED ? gate_logits_kernel<true>
+                                                : gate_logits_kernel<false>;
+  hipLaunchKernelGGL(kern, grid, dim3(64 * kGateWaves), 0, as_stream(stream),
                      reinterpret_cast<const uint16_t*>(x), ld_x,
                      reinterpret_cast<const uint16_t*>(gate_weight), bias, logits, ld_logits, T,
                      E, H);

@@ -1,6 +1,7 @@
 // Fused DeepSeekMoE forward on one GPU: the whole layer (moe.py:77-109) as one
-// C call that enqueues 4-6 kernels on the caller's stream and never waits.
+// C call that enqueues 4-7 kernels on the caller's stream and never waits.
 //
+//   [partial gate sums, dsk_moe_layer_forward only]  ->
 //   route (+histogram, ranks)  ->  [scan + permute when T > 64]  ->
 //   grouped GEMM1 + SwiGLU (A rows gathered from x through token_map)  ->
 //   grouped GEMM2  ->  combine (ascending-expert fp32 sum + shared rows, one
@@ -47,48 +48,15 @@ static FusedLayout fused_layout(int T, int E, int K, int nsh, int H, int I) {
   return L;
 }
 
-}  // namespace dsk
-
-using namespace dsk;
-
-extern "C" size_t dsk_moe_fused_workspace_size(int num_tokens, int num_experts, int top_k,
-                                               int n_shared_groups, int hidden,
-                                               int intermediate) {
-  if (num_tokens < 0 || num_experts <= 0 || top_k <= 0 || n_shared_groups < 0) return 0;
-  return fused_layout(num_tokens, num_experts, top_k, n_shared_groups, hidden, intermediate)
-      .total;
-}
-
-extern "C" int dsk_moe_fused_forward(const float* logits, const dsk_bf16* x, const dsk_bf16* w1,
-                                     const dsk_bf16* w2, dsk_bf16* out, int num_tokens,
-                                     int num_experts, int top_k, int n_shared_groups,
-                                     int hidden, int intermediate, int weight_layout,
-                                     int32_t* topk_idx_out,
-                                     float* topk_w_out, int32_t* expert_offsets_out,
-                                     void* workspace, size_t workspace_bytes,
-                                     void* const* stage_events, void* stream) {
-  const int T = num_tokens, E = num_experts, K = top_k, nsh = n_shared_groups;
-  const int H = hidden, I = intermediate;
-  DSK_REQUIRE(E >= 1 && E <= DSK_MAX_EXPERTS, DSK_ERR_INVALID_ARG,
-              "moe_fused: num_experts must be in [1, 64]");
-  DSK_REQUIRE(K >= 1 && K <= DSK_MAX_TOP_K && K <= E, DSK_ERR_INVALID_ARG,
-              "moe_fused: top_k must be in [1, min(6, num_experts)]");
-  DSK_REQUIRE(nsh >= 0 && E + nsh <= 128, DSK_ERR_INVALID_ARG,
-              "moe_fused: too many shared groups");
-  DSK_REQUIRE(T >= 0, DSK_ERR_INVALID_ARG, "moe_fused: num_tokens < 0");
-  DSK_REQUIRE(H > 0 && H % 64 == 0 && I > 0 && I % 64 == 0, DSK_ERR_INVALID_ARG,
-              "moe_fused: hidden and intermediate sizes must be multiples of 64");
-  DSK_REQUIRE(weight_layout == DSK_LAYOUT_ROW_MAJOR || weight_layout == DSK_LAYOUT_TILED,
-              DSK_ERR_INVALID_ARG, "moe_fused: unknown weight_layout");
-  if (T == 0) return DSK_OK;
-  DSK_REQUIRE(logits && x && w1 && w2 && out, DSK_ERR_NULL_PTR, "moe_fused: NULL pointer");
-  DSK_REQUIRE(aligned16(x) && aligned16(w1) && aligned16(w2) && aligned16(out),
-              DSK_ERR_ALIGNMENT, "moe_fused: tensors must be 16-byte aligned");
-  const FusedLayout L = fused_layout(T, E, K, nsh, H, I);
-  DSK_REQUIRE(workspace != nullptr && workspace_bytes >= L.total && aligned16(workspace),
-              DSK_ERR_WORKSPACE, "moe_fused: workspace too small");
-  hipStream_t st = as_stream(stream);
-  char* ws = static_cast<char*>(workspace);
+// Everything after the gate: route -> permutation -> GEMM1+SwiGLU -> GEMM2 ->
+// combine. The router logits are n_parts partial-sum planes (part_stride
+// floats apart) plus an optional bias, summed by the route kernel.
+static int layer_after_gate(const float* logits, int n_parts, int64_t part_stride,
+                            const float* bias, const uint16_t* x, const uint16_t* w1,
+                            const uint16_t* w2, uint16_t* out, int T, int E, int K, int nsh,
+                            int H, int I, int weight_layout, int32_t* topk_idx_out,
+                            float* topk_w_out, int32_t* expert_offsets_out, char* ws,
+                            const FusedLayout& L, void* const* stage_events, hipStream_t st) {
   int32_t* hist = reinterpret_cast<int32_t*>(ws + L.hist);
   int32_t* base = reinterpret_cast<int32_t*>(ws + L.base);
   int32_t* rank = reinterpret_cast<int32_t*>(ws + L.rank);
@@ -105,7 +73,7 @@ extern "C" int dsk_moe_fused_forward(const float* logits, const dsk_bf16* x, con
   const int Stot = S + nsh * T;
   const int G = E + nsh;
 
-  // optional instrumentation: hipEvent_t recorded at the 5 stage boundaries
+  // optional instrumentation: hipEvent_t recorded at the stage boundaries
   auto mark = [&](int i) -> int {
     if (stage_events == nullptr || stage_events[i] == nullptr) return DSK_OK;
     if (hipEventRecord(reinterpret_cast<hipEvent_t>(stage_events[i]), st) != hipSuccess)
@@ -113,14 +81,13 @@ extern "C" int dsk_moe_fused_forward(const float* logits, const dsk_bf16* x, con
     return DSK_OK;
   };
   int rc;
-  if ((rc = mark(0))) return rc;
   if (nblk == 1) {
-    rc = launch_route(logits, E, T, E, K, idx, w, hist, rank, counts, offsets, token_map,
-                      slot_of, nsh, st);
+    rc = launch_route(logits, E, n_parts, part_stride, bias, T, E, K, idx, w, hist, rank,
+                      counts, offsets, token_map, slot_of, nsh, st);
     if (rc) return rc;
   } else {
-    rc = launch_route(logits, E, T, E, K, idx, w, hist, rank, nullptr, nullptr, nullptr,
-                      nullptr, 0, st);
+    rc = launch_route(logits, E, n_parts, part_stride, bias, T, E, K, idx, w, hist, rank,
+                      nullptr, nullptr, nullptr, nullptr, 0, st);
     if (rc) return rc;
     rc = launch_scan(hist, nblk, E, counts, offsets, base, nsh, T, st);
     if (rc) return rc;
@@ -164,4 +131,115 @@ extern "C" int dsk_moe_fused_forward(const float* logits, const dsk_bf16* x, con
       return fail(DSK_ERR_LAUNCH, "moe_fused: offsets copy failed");
   }
   return DSK_OK;
+}
+
+static int check_layer_args(const char* who, int T, int E, int K, int nsh, int H, int I,
+                            int weight_layout) {
+  const std::string w(who);
+  DSK_REQUIRE(E >= 1 && E <= DSK_MAX_EXPERTS, DSK_ERR_INVALID_ARG,
+              w + ": num_experts must be in [1, 64]");
+  DSK_REQUIRE(K >= 1 && K <= DSK_MAX_TOP_K && K <= E, DSK_ERR_INVALID_ARG,
+              w + ": top_k must be in [1, min(6, num_experts)]");
+  DSK_REQUIRE(nsh >= 0 && E + nsh <= 128, DSK_ERR_INVALID_ARG, w + ": too many shared groups");
+  DSK_REQUIRE(T >= 0, DSK_ERR_INVALID_ARG, w + ": num_tokens < 0");
+  DSK_REQUIRE(H > 0 && H % 64 == 0 && I > 0 && I % 64 == 0, DSK_ERR_INVALID_ARG,
+              w + ": hidden and intermediate sizes must be multiples of 64");
+  DSK_REQUIRE(weight_layout == DSK_LAYOUT_ROW_MAJOR || weight_layout == DSK_LAYOUT_TILED,
+              DSK_ERR_INVALID_ARG, w + ": unknown weight_layout");
+  return DSK_OK;
+}
+
+// Partial gate sums of the layer entry live after the fused layout.
+static size_t layer_parts_offset(int T, int E, int K, int nsh, int H, int I) {
+  return fused_layout(T, E, K, nsh, H, I).total;
+}
+
+}  // namespace dsk
+
+using namespace dsk;
+
+extern "C" size_t dsk_moe_fused_workspace_size(int num_tokens, int num_experts, int top_k,
+                                               int n_shared_groups, int hidden,
+                                               int intermediate) {
+  if (num_tokens < 0 || num_experts <= 0 || top_k <= 0 || n_shared_groups < 0) return 0;
+  return fused_layout(num_tokens, num_experts, top_k, n_shared_groups, hidden, intermediate)
+      .total;
+}
+
+extern "C" int dsk_moe_fused_forward(const float* logits, const dsk_bf16* x, const dsk_bf16* w1,
+                                     const dsk_bf16* w2, dsk_bf16* out, int num_tokens,
+                                     int num_experts, int top_k, int n_shared_groups,
+                                     int hidden, int intermediate, int weight_layout,
+                                     int32_t* topk_idx_out,
+                                     float* topk_w_out, int32_t* expert_offsets_out,
+                                     void* workspace, size_t workspace_bytes,
+                                     void* const* stage_events, void* stream) {
+  const int T = num_tokens, E = num_experts, K = top_k, nsh = n_shared_groups;
+  const int H = hidden, I = intermediate;
+  int rc = check_layer_args("moe_fused", T, E, K, nsh, H, I, weight_layout);
+  if (rc) return rc;
+  if (T == 0) return DSK_OK;
+  DSK_REQUIRE(logits && x && w1 && w2 && out, DSK_ERR_NULL_PTR, "moe_fused: NULL pointer");
+  DSK_REQUIRE(aligned16(x) && aligned16(w1) && aligned16(w2) && aligned16(out),
+              DSK_ERR_ALIGNMENT, "moe_fused: tensors must be 16-byte aligned");
+  const FusedLayout L = fused_layout(T, E, K, nsh, H, I);
+  DSK_REQUIRE(workspace != nullptr && workspace_bytes >= L.total && aligned16(workspace),
+              DSK_ERR_WORKSPACE, "moe_fused: workspace too small");
+  hipStream_t st = as_stream(stream);
+  if (stage_events != nullptr && stage_events[0] != nullptr &&
+      hipEventRecord(reinterpret_cast<hipEvent_t>(stage_events[0]), st) != hipSuccess)
+    return fail(DSK_ERR_LAUNCH, "moe_fused: hipEventRecord failed");
+  return layer_after_gate(logits, 1, 0, nullptr, x, w1, w2, out, T, E, K, nsh, H, I,
+                          weight_layout, topk_idx_out, topk_w_out, expert_offsets_out,
+                          static_cast<char*>(workspace), L, stage_events, st);
+}
+
+extern "C" size_t dsk_moe_layer_workspace_size(int num_tokens, int num_experts, int top_k,
+                                               int n_shared_groups, int hidden,
+                                               int intermediate) {
+  if (num_tokens < 0 || num_experts <= 0 || top_k <= 0 || n_shared_groups < 0 || hidden < 16)
+    return 0;
+  const size_t parts = (size_t)gate_parts_count(num_tokens, num_experts, hidden) *
+                       num_tokens * num_experts * sizeof(float);
+  return layer_parts_offset(num_tokens, num_experts, top_k, n_shared_groups, hidden,
+                            intermediate) + align_up(parts > 0 ? parts : 1, 256);
+}
+
+extern "C" int dsk_moe_layer_forward(const dsk_bf16* x, const dsk_bf16* gate_weight,
+                                     const float* gate_bias, const dsk_bf16* w1,
+                                     const dsk_bf16* w2, dsk_bf16* out, int num_tokens,
+                                     int num_experts, int top_k, int n_shared_groups,
+                                     int hidden, int intermediate, int weight_layout,
+                                     int32_t* topk_idx_out, float* topk_w_out,
+                                     int32_t* expert_offsets_out, void* workspace,
+                                     size_t workspace_bytes, void* const* stage_events,
+                                     void* stream) {
+  const int T = num_tokens, E = num_experts, K = top_k, nsh = n_shared_groups;
+  const int H = hidden, I = intermediate;
+  int rc = check_layer_args("moe_layer", T, E, K, nsh, H, I, weight_layout);
+  if (rc) return rc;
+  DSK_REQUIRE(weight_layout == DSK_LAYOUT_ROW_MAJOR || E % 32 == 0, DSK_ERR_INVALID_ARG,
+              "moe_layer: a tiled gate weight needs num_experts % 32 == 0");
+  if (T == 0) return DSK_OK;
+  DSK_REQUIRE(x && gate_weight && w1 && w2 && out, DSK_ERR_NULL_PTR, "moe_layer: NULL pointer");
+  DSK_REQUIRE(aligned16(x) && aligned16(gate_weight) && aligned16(w1) && aligned16(w2) &&
+                  aligned16(out),
+              DSK_ERR_ALIGNMENT, "moe_layer: tensors must be 16-byte aligned");
+  DSK_REQUIRE(workspace != nullptr && aligned16(workspace) &&
+                  workspace_bytes >= dsk_moe_layer_workspace_size(T, E, K, nsh, H, I),
+              DSK_ERR_WORKSPACE, "moe_layer: workspace too small");
+  hipStream_t st = as_stream(stream);
+  if (stage_events != nullptr && stage_events[0] != nullptr &&
+      hipEventRecord(reinterpret_cast<hipEvent_t>(stage_events[0]), st) != hipSuccess)
+    return fail(DSK_ERR_LAUNCH, "moe_layer: hipEventRecord failed");
+  const FusedLayout L = fused_layout(T, E, K, nsh, H, I);
+  char* ws = static_cast<char*>(workspace);
+  float* parts = reinterpret_cast<float*>(ws + layer_parts_offset(T, E, K, nsh, H, I));
+  const int n_parts = gate_parts_count(T, E, H);
+  rc = launch_gate_parts(x, H, gate_weight, weight_layout == DSK_LAYOUT_TILED, parts, T, E, H,
+                         n_parts, st);
+  if (rc) return rc;
+  return layer_after_gate(parts, n_parts, (int64_t)T * E, gate_bias, x, w1, w2, out, T, E, K,
+                          nsh, H, I, weight_layout, topk_idx_out, topk_w_out,
+                          expert_offsets_out, ws, L, stage_events, st);
 }

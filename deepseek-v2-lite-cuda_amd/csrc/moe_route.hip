@@ -23,17 +23,19 @@ namespace dsk {
 constexpr int kChunk = 64;            // tokens per routing workgroup (= mask width)
 constexpr int kRouteThreads = 1024;   // 16 waves, 4 tokens each
 constexpr int kRouteWaves = kRouteThreads / kWave;
-constexpr int kTokPerWave = kChunk / kRouteWaves;
+constexpr int kTokPerWave = kChunk / kRouteWaves;  // one per 16-lane row
 constexpr int kRankThreads = 256;
+constexpr int kMaxGateParts = 16;  // partial gate-sum planes the route kernel adds
 
 // ------------------------------------------------------------------ route --
-// One wave per token, one expert logit per lane. Writes topk idx / weights,
+// Four tokens per wave (one per 16-lane row). Writes topk idx / weights,
 // the chunk histogram, and (optionally) each (token, k)'s rank inside its chunk.
 // With a single chunk (T <= 64) it also finishes the job that the scan and
 // permutation kernels do for larger T: counts, offsets (including the rows of
 // the always-on groups appended after the routed ones), token_map and slot_of.
 __global__ __launch_bounds__(kRouteThreads) void route_kernel(
-    const float* __restrict__ logits, int64_t ld, int T, int E, int K,
+    const float* __restrict__ logits, int64_t ld, int n_parts, int64_t part_stride,
+    const float* __restrict__ bias, int T, int E, int K,
     int32_t* __restrict__ topk_idx, float* __restrict__ topk_w,
     int32_t* __restrict__ blk_hist, int32_t* __restrict__ local_rank,
     int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
@@ -48,63 +50,87 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(
   __syncthreads();
 
   const int t0 = blockIdx.x * kChunk;
-  // all of this wave's logit loads are issued before any reduction, so their
-  // latency is paid once rather than once per token
-  float xs[kTokPerWave];
+  // Four tokens per wave at once: the 16 lanes of row g hold token
+  // tl = 4 * wave + g, lane j the logits of experts j, j+16, j+32, j+48, so
+  // every reduction is a 4-value local step plus a 16-lane DPP step.
+  const int g = lane >> 4, j = lane & 15;
+  const int tl = kTokPerWave * wave + g;
+  const int t = t0 + tl;
+  const bool active = t < T;  // uniform over the 16-lane row
+  float xv[4];
+  bool taken[4];
+  // logits = sum of n_parts partial sums (K slices of the gate GEMM) in a
+  // fixed order, plus the optional per-expert bias
 #pragma unroll
-  for (int i = 0; i < kTokPerWave; ++i) {
-    const int t = t0 + wave + kRouteWaves * i;
-    xs[i] = (t < T && lane < E) ? logits[(int64_t)t * ld + lane] : -INFINITY;
+  for (int q = 0; q < 4; ++q) {
+    const int e = j + 16 * q;
+    taken[q] = e >= E;  // padding experts are never chosen
+    float v = -INFINITY;
+    if (active && e < E) {
+      // all plane loads issued first, then summed in plane order
+      const float* src = logits + (int64_t)t * ld + e;
+      float pv[kMaxGateParts];
+#pragma unroll
+      for (int s = 0; s < kMaxGateParts; ++s) pv[s] = s < n_parts ? src[s * part_stride] : 0.f;
+      v = pv[0];
+#pragma unroll
+      for (int s = 1; s < kMaxGateParts; ++s)
+        if (s < n_parts) v += pv[s];
+      if (bias != nullptr) v += bias[e];
+    }
+    xv[q] = v;
   }
-  int my_e[kTokPerWave];
+  const float mx = row16_max(fmaxf(fmaxf(xv[0], xv[1]), fmaxf(xv[2], xv[3])));
+  float ex[4];
 #pragma unroll
-  for (int i = 0; i < kTokPerWave; ++i) {
-    my_e[i] = -1;
-    const int tl = wave + kRouteWaves * i;
-    const int t = t0 + tl;
-    if (t < T) {  // wave-uniform
-      const float x = xs[i];
-      const float mx = wave_max(x);
-      const float ex = lane < E ? expf(x - mx) : 0.f;
-      const float sum = wave_sum(ex);
-      const float p = ex / sum;
-      bool taken = lane >= E;
-      int sel_e = -1;
-      float sel_w = 0.f;
-      for (int k = 0; k < K; ++k) {
-        const float v = taken ? -INFINITY : x;
-        const float m = wave_max(v);
-        unsigned long long b = __ballot(!taken && v == m);
-        if (b == 0ull) b = __ballot(!taken);  // NaN logits: lowest untaken index
-        const int e = __builtin_amdgcn_readfirstlane(__ffsll((long long)b) - 1);
-        if (lane == e) taken = true;
-        const float pe = readlane_f(p, e);
-        if (lane == k) {
-          sel_e = e;
-          sel_w = pe;
-        }
-      }
-      if (lane < K) {
-        topk_idx[(int64_t)t * K + lane] = sel_e;
-        topk_w[(int64_t)t * K + lane] = sel_w;
-        atomicOr(&s_mask[sel_e], 1ull << tl);
-        my_e[i] = sel_e;
+  for (int q = 0; q < 4; ++q) ex[q] = taken[q] ? 0.f : expf(xv[q] - mx);
+  const float sum = row16_sum((ex[0] + ex[1]) + (ex[2] + ex[3]));
+  int my_e = -1;       // this lane's pick: k = j (lanes j < K)
+  float my_w = 0.f;
+  // waves whose four rows are all past T skip the selection
+  const bool wave_active = t0 + kTokPerWave * wave < T;
+  for (int k = 0; k < K && wave_active; ++k) {
+    // local best untaken (NaN counts as -inf; ties -> lower expert index)
+    float bv = -INFINITY;
+    int bi = 64;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float v = xv[q] == xv[q] ? xv[q] : -INFINITY;
+      if (!taken[q] && (v > bv || bi == 64)) {
+        bv = v;
+        bi = j + 16 * q;
       }
     }
+    const float m = row16_max(bv);
+    const int win = row16_min((bi < 64 && bv == m) ? bi : 64);
+    // probability of the winner, from its owner lane (j = win % 16)
+    float pw = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (j + 16 * q == win) {
+        taken[q] = true;
+        pw = ex[q] / sum;
+      }
+    pw = __shfl(pw, (lane & ~15) + (win & 15), 64);
+    if (j == k) {
+      my_e = win;
+      my_w = pw;
+    }
+  }
+  if (active && j < K) {
+    topk_idx[(int64_t)t * K + j] = my_e;
+    topk_w[(int64_t)t * K + j] = my_w;
+    atomicOr(&s_mask[my_e], 1ull << tl);
+  } else {
+    my_e = -1;
   }
   __syncthreads();
 
   if (blk_hist != nullptr && tid < E)
     blk_hist[(int64_t)blockIdx.x * E + tid] = __popcll(s_mask[tid]);
 
-  int rank[kTokPerWave];
-#pragma unroll
-  for (int i = 0; i < kTokPerWave; ++i) {
-    const int tl = wave + kRouteWaves * i;
-    rank[i] = my_e[i] >= 0 ? __popcll(s_mask[my_e[i]] & ((1ull << tl) - 1ull)) : -1;
-    if (local_rank != nullptr && my_e[i] >= 0)
-      local_rank[(int64_t)(t0 + tl) * K + lane] = rank[i];
-  }
+  const int rank = my_e >= 0 ? __popcll(s_mask[my_e] & ((1ull << tl) - 1ull)) : -1;
+  if (local_rank != nullptr && my_e >= 0) local_rank[(int64_t)t * K + j] = rank;
 
   if (gridDim.x == 1 && offsets != nullptr) {
     if (wave == 0) {
@@ -117,21 +143,17 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(
       }
       if (lane == 63) {
         offsets[E] = inc;
-        for (int j = 1; j <= n_extra_groups; ++j) offsets[E + j] = inc + j * T;
+        for (int x = 1; x <= n_extra_groups; ++x) offsets[E + x] = inc + x * T;
       }
     }
     if (token_map != nullptr) {
       __syncthreads();
-#pragma unroll
-      for (int i = 0; i < kTokPerWave; ++i) {
-        if (my_e[i] >= 0) {
-          const int t = t0 + wave + kRouteWaves * i;
-          const int slot = s_off[my_e[i]] + rank[i];
-          token_map[slot] = t;
-          if (slot_of != nullptr) slot_of[(int64_t)t * K + lane] = slot;
-        }
+      if (my_e >= 0) {
+        const int slot = s_off[my_e] + rank;
+        token_map[slot] = t;
+        if (slot_of != nullptr) slot_of[(int64_t)t * K + j] = slot;
       }
-      // rows of the always-on groups: group E+j row t is token t
+      // rows of the always-on groups: group E+x row t is token t
       const int S = T * K;
       for (int r = tid; r < n_extra_groups * T; r += kRouteThreads) token_map[S + r] = r % T;
     }
@@ -453,13 +475,14 @@ __global__ void swiglu_scalar_kernel(const uint16_t* __restrict__ in,
 // ------------------------------------------------------------ host helpers --
 static inline int nchunks(int T) { return (T + kChunk - 1) / kChunk; }
 
-int launch_route(const float* logits, int64_t ld, int T, int E, int K, int32_t* idx,
+int launch_route(const float* logits, int64_t ld, int n_parts, int64_t part_stride,
+                 const float* bias, int T, int E, int K, int32_t* idx,
                  float* w, int32_t* blk_hist, int32_t* local_rank, int32_t* counts,
                  int32_t* offsets, int32_t* token_map, int32_t* slot_of,
                  int n_extra_groups, hipStream_t st) {
   hipLaunchKernelGGL(route_kernel, dim3(nchunks(T)), dim3(kRouteThreads), 0, st, logits,
-                     ld, T, E, K, idx, w, blk_hist, local_rank, counts, offsets,
-                     token_map, slot_of, n_extra_groups);
+                     ld, n_parts, part_stride, bias, T, E, K, idx, w, blk_hist, local_rank,
+                     counts, offsets, token_map, slot_of, n_extra_groups);
   return check_launch("route_kernel");
 }
 
@@ -525,16 +548,17 @@ extern "C" int dsk_moe_routing(const float* logits, int64_t ld_logits, int32_t* 
   const int nblk = nchunks(num_tokens);
   if (nblk == 1) {
     // single chunk: the route kernel's own histogram is the count vector
-    return launch_route(logits, ld_logits, num_tokens, num_experts, top_k, topk_idx,
-                        topk_w, expert_counts, nullptr, nullptr, nullptr, nullptr,
+    return launch_route(logits, ld_logits, 1, 0, nullptr, num_tokens, num_experts, top_k,
+                        topk_idx, topk_w, expert_counts, nullptr, nullptr, nullptr, nullptr,
                         nullptr, 0, st);
   }
   DSK_REQUIRE(workspace != nullptr &&
                   workspace_bytes >= dsk_moe_routing_workspace_size(num_tokens, num_experts),
               DSK_ERR_WORKSPACE, "moe_routing: workspace too small");
   int32_t* hist = static_cast<int32_t*>(workspace);
-  int rc = launch_route(logits, ld_logits, num_tokens, num_experts, top_k, topk_idx,
-                        topk_w, hist, nullptr, nullptr, nullptr, nullptr, nullptr, 0, st);
+  int rc = launch_route(logits, ld_logits, 1, 0, nullptr, num_tokens, num_experts, top_k,
+                        topk_idx, topk_w, hist, nullptr, nullptr, nullptr, nullptr, nullptr, 0,
+                        st);
   if (rc) return rc;
   return launch_scan(hist, nblk, num_experts, expert_counts, nullptr, nullptr, 0, 0, st);
 }

@@ -30,6 +30,7 @@ from .moe_fused import (  # noqa: F401
     FusedMoELayer,
     fused_moe_forward,
     moe_fused_forward_logits,
+    moe_layer_forward,
     route_dispatch_combine,
 )
 
@@ -38,5 +39,6 @@ __all__ = [
     "moe_gemm1_swiglu", "moe_gemm2", "rms_norm", "kv_upproj", "linear", "rope",
     "prepack_experts", "prepack_with_shared", "pack_tensors", "tile_weights", "untile_weights",
     "FusedMoELayer",
-    "fused_moe_forward", "moe_fused_forward_logits", "route_dispatch_combine", "DskError",
+    "fused_moe_forward", "moe_fused_forward_logits", "moe_layer_forward",
+    "route_dispatch_combine", "DskError",
 ]

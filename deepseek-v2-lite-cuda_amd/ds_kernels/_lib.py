@@ -25,7 +25,7 @@ _F = ctypes.c_float
 SIGNATURES = {
     "dsk_last_error": (ctypes.c_char_p, []),
     "dsk_abi_version": (_I, []),
-    "dsk_moe_gate_logits": (_I, [_P, _I64, _P, _P, _P, _I64, _I, _I, _I, _P]),
+    "dsk_moe_gate_logits": (_I, [_P, _I64, _P, _P, _P, _I64, _I, _I, _I, _I, _P]),
     "dsk_moe_routing_workspace_size": (_SZ, [_I, _I]),
     "dsk_moe_routing": (_I, [_P, _I64, _P, _P, _P, _I, _I, _I, _P, _SZ, _P]),
     "dsk_moe_scan": (_I, [_P, _P, _I, _P]),
@@ -46,6 +46,9 @@ SIGNATURES = {
                          _P, _P, _I, _I, _I, _I, _I, _P]),
     "dsk_moe_fused_workspace_size": (_SZ, [_I, _I, _I, _I, _I, _I]),
     "dsk_moe_fused_forward": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P,
+                                   _P, _P, _SZ, _P, _P]),
+    "dsk_moe_layer_workspace_size": (_SZ, [_I, _I, _I, _I, _I, _I]),
+    "dsk_moe_layer_forward": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P,
                                    _P, _P, _SZ, _P, _P]),
 }
 

@@ -26,7 +26,41 @@ import torch.nn.functional as F
 
 from . import ops
 from ._lib import check, lib, stream_handle
-from .expert_prepack import prepack_experts, prepack_with_shared
+from .expert_prepack import prepack_experts, prepack_with_shared, tile_weights
+
+
+def _expert_shapes(op: str, w1: torch.Tensor, w2: torch.Tensor):
+    """(tiled, G, 2I, H, w2 logical shape) of row-major or fragment-tiled weights."""
+    tiled = w1.dim() == 5
+    if tiled:
+        if w2.dim() != 5 or tuple(w1.shape[3:]) != (64, 8) or tuple(w2.shape[3:]) != (64, 8):
+            raise RuntimeError(f"{op}: tiled w1/w2 must both be [G, N/32, K/16, 64, 8]")
+        G, N2, Hw = w1.shape[0], w1.shape[1] * 32, w1.shape[2] * 16
+        w2_shape = (w2.shape[0], w2.shape[1] * 32, w2.shape[2] * 16)
+    else:
+        if w1.dim() != 3 or w2.dim() != 3:
+            raise RuntimeError(f"{op}: w1/w2 must be [G, 2I, H] / [G, H, I] (or tiled)")
+        G, N2, Hw = w1.shape
+        w2_shape = tuple(w2.shape)
+    return tiled, G, N2, Hw, w2_shape
+
+
+def _routing_outputs(return_routing: bool, T: int, top_k: int, E: int, dev):
+    if not return_routing:
+        return None, None, None
+    return (torch.empty((T, top_k), dtype=torch.int32, device=dev),
+            torch.empty((T, top_k), dtype=torch.float32, device=dev),
+            torch.empty((E + 1,), dtype=torch.int32, device=dev))
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return t.data_ptr() if t is not None else None
+
+
+def _events(stage_events):
+    if stage_events is not None and not isinstance(stage_events, int):
+        return ctypes.cast(stage_events, ctypes.c_void_p).value
+    return stage_events
 
 
 def moe_fused_forward_logits(logits: torch.Tensor, hidden_states: torch.Tensor,
@@ -46,15 +80,7 @@ def moe_fused_forward_logits(logits: torch.Tensor, hidden_states: torch.Tensor,
     op = "moe_fused_forward"
     T, H = hidden_states.shape
     E = logits.shape[1] if num_experts is None else num_experts
-    tiled = w1.dim() == 5
-    if tiled:
-        if w2.dim() != 5 or tuple(w1.shape[3:]) != (64, 8) or tuple(w2.shape[3:]) != (64, 8):
-            raise RuntimeError(f"{op}: tiled w1/w2 must both be [G, N/32, K/16, 64, 8]")
-        G, N2, Hw = w1.shape[0], w1.shape[1] * 32, w1.shape[2] * 16
-        w2_shape = (w2.shape[0], w2.shape[1] * 32, w2.shape[2] * 16)
-    else:
-        G, N2, Hw = w1.shape
-        w2_shape = tuple(w2.shape)
+    tiled, G, N2, Hw, w2_shape = _expert_shapes(op, w1, w2)
     I = N2 // 2
     for t, n, dt in ((logits, "logits", torch.float32), (hidden_states, "hidden_states", torch.bfloat16),
                      (w1, "w1", torch.bfloat16), (w2, "w2", torch.bfloat16)):
@@ -66,25 +92,70 @@ def moe_fused_forward_logits(logits: torch.Tensor, hidden_states: torch.Tensor,
     dev = hidden_states.device
     out = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
     if T == 0:
-        return out
+        return (out, (None, None, None)) if return_routing else out
     nws = lib.dsk_moe_fused_workspace_size(T, E, top_k, n_shared_groups, H, I)
     ws = workspace if workspace is not None and workspace.numel() >= nws else \
         torch.empty(nws, dtype=torch.uint8, device=dev)
-    if stage_events is not None and not isinstance(stage_events, int):
-        stage_events = ctypes.cast(stage_events, ctypes.c_void_p).value
-    idx = w = offs = None
-    if return_routing:
-        idx = torch.empty((T, top_k), dtype=torch.int32, device=dev)
-        w = torch.empty((T, top_k), dtype=torch.float32, device=dev)
-        offs = torch.empty((E + 1,), dtype=torch.int32, device=dev)
+    idx, w, offs = _routing_outputs(return_routing, T, top_k, E, dev)
     with torch.cuda.device(dev):
         check(lib.dsk_moe_fused_forward(
             logits.data_ptr(), hidden_states.data_ptr(), w1.data_ptr(), w2.data_ptr(),
             out.data_ptr(), T, E, top_k, n_shared_groups, H, I, 1 if tiled else 0,
-            idx.data_ptr() if idx is not None else None,
-            w.data_ptr() if w is not None else None,
-            offs.data_ptr() if offs is not None else None,
-            ws.data_ptr(), ws.numel(), stage_events, stream_handle(dev)), op)
+            _ptr(idx), _ptr(w), _ptr(offs), ws.data_ptr(), ws.numel(), _events(stage_events),
+            stream_handle(dev)), op)
+    if return_routing:
+        return out, (idx, w, offs)
+    return out
+
+
+def moe_layer_forward(hidden_states: torch.Tensor, gate_weight: torch.Tensor,
+                      w1: torch.Tensor, w2: torch.Tensor, top_k: int, n_shared_groups: int,
+                      gate_bias: Optional[torch.Tensor] = None, return_routing: bool = False,
+                      stage_events=None, workspace: Optional[torch.Tensor] = None):
+    """Whole MoE layer from the hidden states, router included (one C call:
+    partial gate sums -> route -> permutation -> GEMM1+SwiGLU -> GEMM2 -> combine).
+
+    gate_weight: bf16 [E, H], in the same layout as w1/w2 (tile_weights(w[None])[0]
+    when they are tiled); gate_bias: optional fp32 [E] added to the logits."""
+    op = "moe_layer_forward"
+    T, H = hidden_states.shape
+    tiled, G, N2, Hw, w2_shape = _expert_shapes(op, w1, w2)
+    I = N2 // 2
+    if tiled:
+        if gate_weight.dim() != 4 or tuple(gate_weight.shape[2:]) != (64, 8):
+            raise RuntimeError(f"{op}: with tiled experts the gate weight must be tiled too")
+        E, Hg = gate_weight.shape[0] * 32, gate_weight.shape[1] * 16
+    else:
+        if gate_weight.dim() != 2:
+            raise RuntimeError(f"{op}: gate_weight must be [experts, hidden]")
+        E, Hg = gate_weight.shape
+    for t, n, dt in ((hidden_states, "hidden_states", torch.bfloat16),
+                     (gate_weight, "gate_weight", torch.bfloat16),
+                     (w1, "w1", torch.bfloat16), (w2, "w2", torch.bfloat16)):
+        if not (t.is_cuda and t.is_contiguous() and t.dtype == dt):
+            raise RuntimeError(f"{op}: {n} must be a contiguous CUDA {dt} tensor")
+    if gate_bias is not None and not (gate_bias.is_cuda and gate_bias.dtype == torch.float32
+                                      and tuple(gate_bias.shape) == (E,)):
+        raise RuntimeError(f"{op}: gate_bias must be a CUDA float32 tensor of shape [{E}]")
+    if Hg != H or G != E + n_shared_groups or Hw != H or w2_shape != (G, H, I):
+        raise RuntimeError(f"{op}: inconsistent shapes x={tuple(hidden_states.shape)} "
+                           f"gate={tuple(gate_weight.shape)} w1={tuple(w1.shape)} "
+                           f"w2={tuple(w2.shape)}")
+    dev = hidden_states.device
+    out = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+    if T == 0:
+        return (out, (None, None, None)) if return_routing else out
+    nws = lib.dsk_moe_layer_workspace_size(T, E, top_k, n_shared_groups, H, I)
+    ws = workspace if workspace is not None and workspace.numel() >= nws else \
+        torch.empty(nws, dtype=torch.uint8, device=dev)
+    idx, w, offs = _routing_outputs(return_routing, T, top_k, E, dev)
+    bias = gate_bias.contiguous() if gate_bias is not None else None
+    with torch.cuda.device(dev):
+        check(lib.dsk_moe_layer_forward(
+            hidden_states.data_ptr(), gate_weight.data_ptr(), _ptr(bias), w1.data_ptr(),
+            w2.data_ptr(), out.data_ptr(), T, E, top_k, n_shared_groups, H, I,
+            1 if tiled else 0, _ptr(idx), _ptr(w), _ptr(offs), ws.data_ptr(), ws.numel(),
+            _events(stage_events), stream_handle(dev)), op)
     if return_routing:
         return out, (idx, w, offs)
     return out
@@ -95,7 +166,7 @@ def gate_logits(hidden_states: torch.Tensor, gate_weight: torch.Tensor,
     """fp32 router logits [T, E]: the gate kernel for a bf16 gate weight, else
     torch's fp32 linear (the reference's own formula)."""
     if gate_weight.dtype == torch.bfloat16 and hidden_states.dtype == torch.bfloat16:
-        return ops.moe_gate(hidden_states, gate_weight, bias)
+        return ops.moe_gate(hidden_states, gate_weight, bias)   # row-major or tiled weight
     logits = F.linear(hidden_states.float(), gate_weight.float(), None)
     return logits + bias if bias is not None else logits
 
@@ -131,6 +202,9 @@ class FusedMoELayer(nn.Module):
             raise ValueError("FusedMoELayer: moe_module must have 'gate' and 'experts' attributes.")
         dev = device if device is not None else moe_module.gate.weight.device
         self.gate_weight = moe_module.gate.weight.detach().to(dev)
+        if self.gate_weight.dtype == torch.bfloat16 and self.gate_weight.shape[0] % 32 == 0:
+            # fragment-tiled for the gate kernel (coalesced weight loads)
+            self.gate_weight = tile_weights(self.gate_weight[None])[0]
         self.top_k = int(moe_module.num_experts_per_tok)
         self.num_experts = len(moe_module.experts)
         shared = getattr(moe_module, "shared_experts", None)
@@ -142,9 +216,14 @@ class FusedMoELayer(nn.Module):
         assert hidden_states.dtype == torch.bfloat16, "hidden_states must be BF16."
         orig = hidden_states.shape
         x = hidden_states.reshape(-1, orig[-1]).contiguous()
-        logits = gate_logits(x, self.gate_weight)
-        out = moe_fused_forward_logits(logits, x, self.w1, self.w2, self.top_k,
-                                       self.n_shared_groups, self.num_experts)
+        if self.gate_weight.dtype == torch.bfloat16 and (self.w1.dim() == 5) == (
+                self.gate_weight.dim() == 4):
+            out = moe_layer_forward(x, self.gate_weight, self.w1, self.w2, self.top_k,
+                                    self.n_shared_groups)   # gate + layer, one call
+        else:
+            logits = gate_logits(x, self.gate_weight)
+            out = moe_fused_forward_logits(logits, x, self.w1, self.w2, self.top_k,
+                                           self.n_shared_groups, self.num_experts)
         return out.view(orig)
 
 

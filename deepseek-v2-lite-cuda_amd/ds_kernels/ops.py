@@ -52,8 +52,14 @@ def moe_gate(x: torch.Tensor, weight: torch.Tensor,
     _req(x.dim() == 2 and x.stride(1) == 1, f"{op}: x must be [tokens, hidden] with unit column stride.")
     _cuda_contig(weight, "weight", op)
     T, H = x.shape
-    E = weight.shape[0]
-    _req(weight.dim() == 2 and weight.shape[1] == H, f"{op}: weight must be [experts, {H}].")
+    tiled = weight.dim() == 4   # [E/32, H/16, 64, 8] from tile_weights(w[None])[0]
+    if tiled:
+        _req(tuple(weight.shape[2:]) == (64, 8) and weight.shape[1] * 16 == H,
+             f"{op}: tiled weight must be [experts/32, {H // 16}, 64, 8].")
+        E = weight.shape[0] * 32
+    else:
+        E = weight.shape[0]
+        _req(weight.dim() == 2 and weight.shape[1] == H, f"{op}: weight must be [experts, {H}].")
     _req(E <= MAX_EXPERTS, "num_experts must not exceed 64.")
     if bias is not None:
         _cuda_contig(bias, "bias", op)
@@ -64,7 +70,8 @@ def moe_gate(x: torch.Tensor, weight: torch.Tensor,
     with torch.cuda.device(dev):
         check(lib.dsk_moe_gate_logits(x.data_ptr(), x.stride(0), weight.data_ptr(),
                                       bias.data_ptr() if bias is not None else None,
-                                      logits.data_ptr(), E, T, E, H, stream_handle(dev)), op)
+                                      logits.data_ptr(), E, T, E, H, 1 if tiled else 0,
+                                      stream_handle(dev)), op)
     return logits
 
 

@@ -60,11 +60,14 @@ int dsk_abi_version(void);
  * summation order fixed by this kernel (results differ from torch's only by
  * fp32 rounding). The optional bias is a per-expert routing bias added to the
  * logits (the Zipf-skewed router of BASELINE config 2 is such a bias).
- * x: bf16 [T, H] row stride ld_x; gate_weight: bf16 [E, H] contiguous;
+ * x: bf16 [T, H] row stride ld_x; gate_weight: bf16 [E, H], row-major
+ * (DSK_LAYOUT_ROW_MAJOR) or fragment-tiled like the expert weights of
+ * dsk_moe_fused_forward (DSK_LAYOUT_TILED, E % 32 == 0);
  * logits: fp32 [T, E] row stride ld_logits. E <= 64, H % 16 == 0. */
 int dsk_moe_gate_logits(const dsk_bf16* x, int64_t ld_x, const dsk_bf16* gate_weight,
                         const float* bias, float* logits, int64_t ld_logits,
-                        int num_tokens, int num_experts, int hidden, void* stream);
+                        int num_tokens, int num_experts, int hidden,
+                        int weight_layout, void* stream);
 
 /* ---------------------------------------------------------------- routing --
  * Softmax over E expert logits + top-K (ties -> lower expert index, emitted in
@@ -233,6 +236,28 @@ int dsk_moe_fused_forward(const float* logits, const dsk_bf16* x,
                           float* topk_w_out, int32_t* expert_offsets_out,
                           void* workspace, size_t workspace_bytes,
                           void* const* stage_events, void* stream);
+
+/* The same layer from the hidden states, gate included: the router logits
+ * x @ gate_weight^T (+ gate_bias) are computed in fp32 from bf16 inputs (as
+ * dsk_moe_gate_logits), as partial sums over K slices that the route kernel
+ * adds in a fixed order, then the layer runs as dsk_moe_fused_forward.
+ * Replaces the whole FusedMoELayer.forward of the reference
+ * (moe_fused.py:197-216) including its fp32 gate linear (moe_fused.py:131).
+ * gate_weight: bf16 [E, H], in the layout weight_layout names for w1/w2
+ * (tiled needs E % 32 == 0); gate_bias: optional fp32 [E]. stage_events[0]
+ * is recorded before the gate. */
+size_t dsk_moe_layer_workspace_size(int num_tokens, int num_experts,
+                                    int top_k, int n_shared_groups,
+                                    int hidden, int intermediate);
+int dsk_moe_layer_forward(const dsk_bf16* x, const dsk_bf16* gate_weight,
+                          const float* gate_bias, const dsk_bf16* w1,
+                          const dsk_bf16* w2, dsk_bf16* out, int num_tokens,
+                          int num_experts, int top_k, int n_shared_groups,
+                          int hidden, int intermediate, int weight_layout,
+                          int32_t* topk_idx_out, float* topk_w_out,
+                          int32_t* expert_offsets_out, void* workspace,
+                          size_t workspace_bytes, void* const* stage_events,
+                          void* stream);
 
 #ifdef __cplusplus
 }

@@ -85,16 +85,18 @@ def test_norm_rope_validation(dsk):
 
 def test_gate_validation(dsk):
     lib = dsk.lib
-    rc = lib.dsk_moe_gate_logits(16, 2048, 16, None, 16, 65, 4, 65, 2048, None)
+    rc = lib.dsk_moe_gate_logits(16, 2048, 16, None, 16, 65, 4, 65, 2048, 0, None)
     assert rc == 1 and "64" in _err(dsk)
-    rc = lib.dsk_moe_gate_logits(16, 2048, 16, None, 16, 64, 4, 64, 2040, None)
+    rc = lib.dsk_moe_gate_logits(16, 2048, 16, None, 16, 64, 4, 64, 2040, 0, None)
     assert rc == 1 and "16" in _err(dsk)
-    rc = lib.dsk_moe_gate_logits(None, 2048, 16, None, 16, 64, 4, 64, 2048, None)
+    rc = lib.dsk_moe_gate_logits(None, 2048, 16, None, 16, 64, 4, 64, 2048, 0, None)
     assert rc == 2
-    rc = lib.dsk_moe_gate_logits(16, 2052, 16, None, 16, 64, 4, 64, 2048, None)
+    rc = lib.dsk_moe_gate_logits(16, 2052, 16, None, 16, 64, 4, 64, 2048, 0, None)
     assert rc == 3
-    rc = lib.dsk_moe_gate_logits(16, 2040, 16, None, 16, 64, 4, 64, 2048, None)
+    rc = lib.dsk_moe_gate_logits(16, 2040, 16, None, 16, 64, 4, 64, 2048, 0, None)
     assert rc == 1 and "stride" in _err(dsk)
+    rc = lib.dsk_moe_gate_logits(16, 2048, 16, None, 16, 40, 4, 40, 2048, 1, None)
+    assert rc == 1 and "tiled" in _err(dsk)
 
 
 def test_fused_validation_and_workspace_sizes(dsk):
@@ -112,6 +114,21 @@ def test_fused_validation_and_workspace_sizes(dsk):
     rc = lib.dsk_moe_fused_forward(16, 16, 16, 16, 16, 4, 64, 6, 2, 2048, 1408, 7, None, None,
                                    None, None, 0, None, None)
     assert rc == 1 and "weight_layout" in _err(dsk)
+
+
+def test_layer_forward_validation(dsk):
+    lib = dsk.lib
+    assert lib.dsk_moe_layer_workspace_size(16, 64, 6, 2, 2048, 1408) > \
+        lib.dsk_moe_fused_workspace_size(16, 64, 6, 2, 2048, 1408)
+    rc = lib.dsk_moe_layer_forward(16, 16, None, 16, 16, 16, 4, 40, 6, 2, 2048, 1408, 1,
+                                   None, None, None, 16, 1 << 30, None, None)
+    assert rc == 1 and "% 32" in _err(dsk)
+    rc = lib.dsk_moe_layer_forward(16, None, None, 16, 16, 16, 4, 64, 6, 2, 2048, 1408, 1,
+                                   None, None, None, 16, 1 << 30, None, None)
+    assert rc == 2
+    rc = lib.dsk_moe_layer_forward(16, 16, None, 16, 16, 16, 4, 64, 6, 2, 2048, 1408, 1,
+                                   None, None, None, 16, 1024, None, None)
+    assert rc == 5
 
 
 def test_python_ops_reject_cpu_tensors(dsk):

@@ -46,6 +46,9 @@ def test_gate_logits_match_fp64(dsk, T, E, H, bias):
     err = np.abs(out.cpu().double().numpy() - ref).max() / np.abs(ref).max()
     assert err <= F32_TOL, err
     assert torch.equal(out, dsk.moe_gate(xd, wg.to(DEV), b.to(DEV) if b is not None else None))
+    if E % 32 == 0:   # fragment-tiled gate weight: same sums, same bits
+        wt = dsk.tile_weights(wg[None])[0].to(DEV)
+        assert torch.equal(out, dsk.moe_gate(xd, wt, b.to(DEV) if b is not None else None))
 
 
 def test_gate_logits_strided_rows(dsk):
@@ -312,6 +315,40 @@ def test_fused_layer_matches_oracle(dsk, full_layer, tiled_layer, T, bias, layou
     err = max_rel_err(np32(out), ref)
     assert err <= BF16_TOL, err
     out2 = dsk.moe_fused_forward_logits(logits, xd, w1, w2, 6, nsh, 64)
+    assert torch.equal(out, out2)
+
+
+@pytest.mark.parametrize("layout", ["row_major", "tiled"])
+@pytest.mark.parametrize("T,bias", [(1, True), (16, True), (64, True), (100, False),
+                                    (4096, False)])
+def test_layer_forward_with_gate_matches_oracle(dsk, full_layer, tiled_layer, T, bias, layout):
+    """Gate included (partial K-slice sums added by the router): routing equals the
+    oracle's on the fp64 logits of the same bf16 inputs (the seeded inputs have no
+    near-ties), the layer output is within the bf16 bar."""
+    from ds_kernels import synthetic as syn
+    W, w1, w2, nsh, Wn = full_layer
+    wg = W.wg.to(torch.bfloat16)
+    if layout == "tiled":
+        w1, w2 = tiled_layer
+        wgd = dsk.tile_weights(wg[None])[0].to(DEV)
+    else:
+        wgd = wg.to(DEV)
+    x = syn.tokens(T).to(torch.bfloat16)
+    b = syn.zipf_router_bias() if bias else None
+    out, (idx, w, off) = dsk.moe_layer_forward(x.to(DEV), wgd, w1, w2, 6, nsh,
+                                               gate_bias=b.to(DEV) if bias else None,
+                                               return_routing=True)
+    lg = x.double().numpy() @ wg.double().numpy().T
+    if bias:
+        lg = lg + b.double().numpy()
+    ridx, rw, rcounts = om.route(lg.astype(np.float32), 6)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+    np.testing.assert_array_equal(off.cpu().numpy(), om.scan(rcounts))
+    np.testing.assert_allclose(np32(w), rw, rtol=1e-5, atol=1e-7)
+    ref = _oracle_layer(Wn, x, lg.astype(np.float32), 6)
+    assert max_rel_err(np32(out), ref) <= BF16_TOL
+    out2 = dsk.moe_layer_forward(x.to(DEV), wgd, w1, w2, 6, nsh,
+                                 gate_bias=b.to(DEV) if bias else None)
     assert torch.equal(out, out2)
 
 
