@@ -140,6 +140,76 @@ def bench_decode(dsk, syn, torch, F, W, packed, T, steps, ev, copies):
             "algorithmic_bytes": bytes_, "GB/s": gbs, "frac_of_8TB/s": gbs / PEAK_HBM_GBS}
 
 
+def bench_mla(dsk, syn, torch, ev, reps=20, warmup=5):
+    """BASELINE configs 3 and 4: the MLA projection block at 8 x 2048 (rms_norm and
+    rope against HBM, kv_upproj against MFMA, each timed with HIP events on the
+    launch stream) and the full decoder layer at 4 x 2048 (tokens/s)."""
+    from ds_kernels import mla as dm
+    dev = torch.device("cuda:0")
+    W = dm.MLAWeights.from_tensors(syn.mla_weights(), dev)
+    b, s, H = 8, 2048, 2048
+    g = torch.Generator().manual_seed(1234)
+    x = torch.randn(b, s, H, generator=g).to(torch.bfloat16).to(dev)
+    cos, sin = dm.yarn_cos_sin(s, device=dev)
+    cb = cos.to(torch.bfloat16)[None, None].expand(b, 1, s, 64)
+    sb = sin.to(torch.bfloat16)[None, None].expand(b, 1, s, 64)
+    q = dsk.linear(x, W.q).view(b, s, 16, 192).transpose(1, 2)
+    kva = dsk.linear(x, W.kva)
+    latent = dsk.rms_norm(kva[..., :512], W.kva_norm)
+    k_pe = kva[..., 512:].view(b, s, 1, 64).transpose(1, 2)
+    st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        evs = ev.create(2 * reps)
+        for i in range(reps):
+            ev.rt.hipEventRecord(evs[2 * i], st())
+            fn()
+            ev.rt.hipEventRecord(evs[2 * i + 1], st())
+        torch.cuda.synchronize()
+        t = sorted(ev.ms(evs[2 * i], evs[2 * i + 1]) for i in range(reps))
+        ev.destroy(evs)
+        return t[len(t) // 2]
+
+    rows = b * s
+    t_norm = timed(lambda: dsk.rms_norm(kva[..., :512], W.kva_norm))
+    t_rope = timed(lambda: dsk.rope(q[..., 128:], k_pe, cb, sb))
+    t_kvb = timed(lambda: dsk.kv_upproj(latent, W.kvb))
+    t_block = timed(lambda: dm.mla_projections(x, W, cos, sin))
+    norm_bytes = 2 * rows * 512 * 2 + 512 * 4
+    rope_bytes = 2 * (rows * 16 * 64 * 2) + 2 * (rows * 64 * 2) + 2 * (s * 64 * 2)
+    kvb_flops = 2.0 * rows * 512 * 4096
+    kvb_bytes = rows * 512 * 2 + 4096 * 512 * 2 + rows * 4096 * 2
+    gbs = lambda nbytes, ms: nbytes / (ms * 1e-3) / 1e9  # noqa: E731
+    out = {
+        "config3_projection_block": {
+            "shape": "b=8, s=2048: q 2048->3072, kv_a 2048->576, rms_norm(512, strided), "
+                     "kv_b 512->4096, rope(q 16 heads + k, 64 dims)",
+            "block_ms": t_block, "tokens_per_s": rows / (t_block * 1e-3),
+            "rms_norm": {"us": t_norm * 1e3, "algorithmic_bytes": norm_bytes,
+                         "GB/s": gbs(norm_bytes, t_norm),
+                         "frac_of_8TB/s": gbs(norm_bytes, t_norm) / PEAK_HBM_GBS},
+            "rope": {"us": t_rope * 1e3, "algorithmic_bytes": rope_bytes,
+                     "GB/s": gbs(rope_bytes, t_rope),
+                     "frac_of_8TB/s": gbs(rope_bytes, t_rope) / PEAK_HBM_GBS},
+            "kv_upproj": {"us": t_kvb * 1e3, "flops": kvb_flops,
+                          "TFLOP/s": kvb_flops / (t_kvb * 1e-3) / 1e12,
+                          "frac_of_bf16_peak": kvb_flops / (t_kvb * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+                          "GB/s": gbs(kvb_bytes, t_kvb)},
+        }}
+    del q, kva, latent, k_pe
+    # config 4: the decoder layer at 4 x 2048
+    P = dm.DecoderLayerWeights.from_tensors(syn.mla_weights(), syn.moe_weights(), dev)
+    b4 = 4
+    x4 = torch.randn(b4, s, H, generator=g).to(torch.bfloat16).to(dev)
+    t_layer = timed(lambda: dm.decoder_layer_forward(x4, P, cos, sin))
+    out["config4_decoder_layer"] = {
+        "shape": "b=4, s=2048, causal; MLA (16 heads) + MoE (64 routed top-6 + 2 shared)",
+        "layer_ms": t_layer, "tokens_per_s": b4 * s / (t_layer * 1e-3)}
+    return out
+
+
 def cpu_baseline(W, syn, budget_s):
     import numpy as np
     from oracle import moe as om
@@ -314,6 +384,8 @@ def main():
         out["decode"] = [bench_decode(dsk, syn, torch, F, W, packed, t, args.decode_steps, ev,
                                       copies) for t in (1, 4, 16, 64)]
         del copies
+        print("bench: mla block and decoder layer", file=sys.stderr, flush=True)
+        out["mla"] = bench_mla(dsk, syn, torch, ev)
         print("bench: cpu baseline", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline(W, syn, args.cpu_seconds)
     print(json.dumps(out), flush=True)

@@ -1,0 +1,171 @@
+"""DeepSeek-V2-Lite MLA projection block and decoder layer composed from this
+package's kernels (reference: src/reference/mla.py:251-393 DeepSeekMLA,
+src/reference/decoder_layer.py:108-139 DeepSeekDecoderLayer).
+
+Kernels used: `linear` (MFMA GEMM) for q_proj, kv_a_proj_with_mqa and o_proj,
+`rms_norm` straight on the 512-wide latent slice of the 576-wide kv_a output
+(row-strided, no copy), `kv_upproj`, `rope` on strided q_pe / k_pe views with
+the position tables broadcast over the batch (no materialised copies), and the
+fused MoE layer (`moe_layer_forward`). The causal attention core stays torch,
+as the survey scopes it, computed in fp32 with contiguous operands.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Optional, Tuple
+
+import torch
+
+from . import ops
+from .expert_prepack import pack_tensors, tile_weights
+from .moe_fused import moe_layer_forward
+
+
+# ------------------------------------------------------------- YaRN tables --
+def _yarn_correction_dim(num_rotations: float, dim: int, base: float, max_pos: int) -> float:
+    return (dim * math.log(max_pos / (num_rotations * 2 * math.pi))) / (2 * math.log(base))
+
+
+def _yarn_mscale(scale: float, mscale: float) -> float:
+    return 1.0 if scale <= 1 else 0.1 * mscale * math.log(scale) + 1.0
+
+
+def yarn_cos_sin(seq_len: int, dim: int = 64, base: float = 10000.0, factor: float = 40.0,
+                 original_max_position: int = 4096, beta_fast: int = 32, beta_slow: int = 1,
+                 mscale: float = 0.707, mscale_all_dim: float = 0.707,
+                 device: Optional[torch.device] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """cos/sin tables [seq_len, dim] fp32 of YaRNRotaryEmbedding (mla.py:108-165):
+    inv_freq blends base^(-2i/d) and base^(-2i/d)/factor over the linear ramp
+    between the correction dims of beta_fast and beta_slow; emb = cat(freqs,
+    freqs); the tables are scaled by mscale(factor, mscale)/mscale(factor, all)."""
+    pos = torch.arange(0, dim, 2, dtype=torch.float32) / dim
+    extra = 1.0 / (base ** pos)
+    inter = 1.0 / (factor * base ** pos)
+    lo = max(math.floor(_yarn_correction_dim(beta_fast, dim, base, original_max_position)), 0)
+    hi = min(math.ceil(_yarn_correction_dim(beta_slow, dim, base, original_max_position)),
+             dim - 1)
+    if lo == hi:
+        hi += 0.001
+    ramp = ((torch.arange(dim // 2, dtype=torch.float32) - lo) / (hi - lo)).clamp(0, 1)
+    keep = 1.0 - ramp
+    inv_freq = inter * (1.0 - keep) + extra * keep
+    m = _yarn_mscale(factor, mscale) / _yarn_mscale(factor, mscale_all_dim)
+    t = torch.arange(seq_len, dtype=torch.float32)
+    freqs = torch.outer(t, inv_freq)
+    emb = torch.cat([freqs, freqs], dim=-1)
+    cos, sin = emb.cos() * m, emb.sin() * m
+    if device is not None:
+        cos, sin = cos.to(device), sin.to(device)
+    return cos, sin
+
+
+# ----------------------------------------------------------------- weights --
+@dataclass
+class MLAWeights:
+    """bf16 projection weights ([out, in], nn.Linear order) and the fp32 latent norm."""
+    q: torch.Tensor          # [heads*(nope+rope), H]
+    kva: torch.Tensor        # [kv_lora+rope, H]
+    kva_norm: torch.Tensor   # [kv_lora] fp32
+    kvb: torch.Tensor        # [heads*(nope+v), kv_lora]
+    o: torch.Tensor          # [H, heads*v]
+    n_heads: int = 16
+    nope: int = 128
+    rope_dim: int = 64
+    v_dim: int = 128
+    kv_lora: int = 512
+    factor: float = 40.0     # YaRN scaling factor of DeepSeek-V2-Lite
+
+    @staticmethod
+    def from_tensors(w: dict, device: torch.device) -> "MLAWeights":
+        bf = lambda t: t.to(device=device, dtype=torch.bfloat16).contiguous()  # noqa: E731
+        return MLAWeights(q=bf(w["q"]), kva=bf(w["kva"]),
+                          kva_norm=w["kva_norm"].to(device=device, dtype=torch.float32),
+                          kvb=bf(w["kvb"]), o=bf(w["o"]))
+
+    @property
+    def softmax_scale(self) -> float:
+        """mla.py:287-288: (nope + rope)^-0.5 * mscale(factor, 0.707)^2."""
+        m = _yarn_mscale(self.factor, 0.707)
+        return (self.nope + self.rope_dim) ** -0.5 * m * m
+
+
+# ------------------------------------------------------------- projections --
+def mla_projections(x: torch.Tensor, W: MLAWeights, cos: torch.Tensor, sin: torch.Tensor,
+                    eps: float = 1e-6):
+    """The projection block of DeepSeekMLA.forward (mla.py:318-352, BASELINE
+    config 3). x: bf16 [b, s, H]; cos/sin: bf16 [s, rope_dim] for positions 0..s-1.
+    Returns (q_nope [b,h,s,nope], q_rot [b,h,s,r], k_nope [b,h,s,nope],
+    v [b,h,s,v], k_rot [b,1,s,r], latent_normed [b,s,kv_lora]); q_nope, k_nope
+    and v are strided views of the projection outputs."""
+    b, s, _ = x.shape
+    h, nope, r, vd, lora = W.n_heads, W.nope, W.rope_dim, W.v_dim, W.kv_lora
+    q = ops.linear(x, W.q).view(b, s, h, nope + r).transpose(1, 2)     # [b,h,s,192] view
+    kva = ops.linear(x, W.kva)                                         # [b,s,576]
+    latent = ops.rms_norm(kva[..., :lora], W.kva_norm, eps)            # strided rows, no copy
+    kv = ops.kv_upproj(latent, W.kvb).view(b, s, h, nope + vd).transpose(1, 2)
+    k_pe = kva[..., lora:].view(b, s, 1, r).transpose(1, 2)           # [b,1,s,64] view
+    cb = cos.to(torch.bfloat16)[None, None].expand(b, 1, s, r)         # batch stride 0
+    sb = sin.to(torch.bfloat16)[None, None].expand(b, 1, s, r)
+    q_rot, k_rot = ops.rope(q[..., nope:], k_pe, cb, sb)
+    return q[..., :nope], q_rot, kv[..., :nope], kv[..., nope:], k_rot, latent
+
+
+def mla_forward(x: torch.Tensor, W: MLAWeights, cos: torch.Tensor, sin: torch.Tensor,
+                eps: float = 1e-6) -> torch.Tensor:
+    """DeepSeekMLA.forward (mla.py:295-393) for positions 0..s-1 with the causal
+    mask: projections on this package's kernels, attention core in fp32 torch,
+    o_proj on the MFMA GEMM. x: bf16 [b, s, H] -> bf16 [b, s, H]."""
+    b, s, H = x.shape
+    q_nope, q_rot, k_nope, v, k_rot, _ = mla_projections(x, W, cos, sin, eps)
+    q = torch.cat([q_nope, q_rot], dim=-1).float()
+    k = torch.cat([k_nope, k_rot.expand(b, W.n_heads, s, W.rope_dim)], dim=-1).float()
+    scores = torch.matmul(q, k.transpose(-1, -2).contiguous()) * W.softmax_scale
+    causal = torch.ones(s, s, dtype=torch.bool, device=x.device).triu(1)
+    scores.masked_fill_(causal, float("-inf"))
+    p = torch.softmax(scores, dim=-1)
+    o = torch.matmul(p, v.float().contiguous())                        # [b,h,s,v]
+    o = o.transpose(1, 2).reshape(b, s, W.n_heads * W.v_dim).to(torch.bfloat16)
+    return ops.linear(o, W.o)
+
+
+# ------------------------------------------------------------ decoder layer --
+@dataclass
+class DecoderLayerWeights:
+    mla: MLAWeights
+    in_norm: torch.Tensor      # [H] fp32
+    post_norm: torch.Tensor    # [H] fp32
+    gate: torch.Tensor         # tiled bf16 router weight
+    w1: torch.Tensor           # tiled [G, 2I/32, H/16, 64, 8]
+    w2: torch.Tensor           # tiled [G, H/32, I/16, 64, 8]
+    n_shared_groups: int
+    top_k: int = 6
+
+    @staticmethod
+    def from_tensors(mla_w: dict, moe_w, device: torch.device,
+                     in_norm: Optional[torch.Tensor] = None,
+                     post_norm: Optional[torch.Tensor] = None) -> "DecoderLayerWeights":
+        """mla_w: synthetic.mla_weights() layout; moe_w: synthetic.moe_weights()."""
+        H = moe_w.wg.shape[1]
+        w1, w2, nsh = pack_tensors(moe_w.gates, moe_w.ups, moe_w.downs, device=device,
+                                   shared=moe_w.shared)
+        gate = tile_weights(moe_w.wg.to(torch.bfloat16)[None])[0].to(device)
+        ones = torch.ones(H, dtype=torch.float32)
+        return DecoderLayerWeights(
+            mla=MLAWeights.from_tensors(mla_w, device),
+            in_norm=(in_norm if in_norm is not None else ones).to(device, torch.float32),
+            post_norm=(post_norm if post_norm is not None else ones).to(device, torch.float32),
+            gate=gate, w1=tile_weights(w1), w2=tile_weights(w2), n_shared_groups=nsh)
+
+
+def decoder_layer_forward(x: torch.Tensor, P: DecoderLayerWeights, cos: torch.Tensor,
+                          sin: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """DeepSeekDecoderLayer.forward (decoder_layer.py:108-139), BASELINE config 4:
+    RMSNorm -> MLA (causal) -> residual -> RMSNorm -> MoE (routed + shared) ->
+    residual. x: bf16 [b, s, H]."""
+    b, s, H = x.shape
+    h = ops.rms_norm(x, P.in_norm, eps)
+    x = x + mla_forward(h, P.mla, cos, sin, eps)
+    h = ops.rms_norm(x, P.post_norm, eps)
+    m = moe_layer_forward(h.reshape(-1, H), P.gate, P.w1, P.w2, P.top_k, P.n_shared_groups)
+    return x + m.view(b, s, H)

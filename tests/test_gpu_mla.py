@@ -102,3 +102,67 @@ def test_linear(dsk, M, K, N):
     out = dsk.linear(x.to(DEV), w.to(DEV))
     ref = np32(x) @ np32(w).T
     assert max_rel_err(np32(out), ref) <= BF16_TOL
+
+
+# ------------------------------------------- configs 3 and 4 (composition) --
+def _bf(t):
+    return t.to(torch.bfloat16).float().numpy()
+
+
+@pytest.fixture(scope="module")
+def mla_setup(dsk):
+    from ds_kernels import mla as dm
+    from ds_kernels import synthetic as syn
+    w = syn.mla_weights()
+    W = dm.MLAWeights.from_tensors(w, torch.device(DEV))
+    wn = {k: (_bf(v) if k != "kva_norm" else v.numpy()) for k, v in w.items()}
+    return dm, w, W, wn
+
+
+def test_mla_projections_match_oracle(mla_setup):
+    """Config 3's projection block (b=2, s=128 here): every output within the bf16 bar."""
+    dm, w, W, wn = mla_setup
+    b, s = 2, 128
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(b, s, 2048, generator=g).to(torch.bfloat16)
+    cos, sin = dm.yarn_cos_sin(s)
+    outs = dm.mla_projections(x.to(DEV), W, cos.to(DEV), sin.to(DEV))
+    cb, sb = _bf(cos), _bf(sin)
+    refs = ol.mla_projections(np32(x), wn["q"], wn["kva"], wn["kva_norm"], wn["kvb"], cb, sb)
+    names = ["q_nope", "q_rot", "k_nope", "v", "k_rot", "latent"]
+    for name, o, r in zip(names, outs, refs):
+        assert tuple(o.shape) == r.shape, name
+        assert max_rel_err(np32(o), r) <= BF16_TOL, name
+
+
+def test_mla_forward_matches_oracle(mla_setup):
+    dm, w, W, wn = mla_setup
+    b, s = 1, 128
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(b, s, 2048, generator=g).to(torch.bfloat16)
+    cos, sin = dm.yarn_cos_sin(s)
+    out = dm.mla_forward(x.to(DEV), W, cos.to(DEV), sin.to(DEV))
+    ref = ol.mla_forward(np32(x), wn["q"], wn["kva"], wn["kva_norm"], wn["kvb"], wn["o"])
+    assert out.shape == (b, s, 2048)
+    assert max_rel_err(np32(out), ref) <= BF16_TOL
+
+
+def test_decoder_layer_matches_oracle(mla_setup):
+    """Config 4's layer at b=1, s=64: RMSNorm -> MLA -> residual -> RMSNorm ->
+    MoE (64 routed top-6 + 2 shared) -> residual, against the fp32 oracle."""
+    dm, w, W, wn = mla_setup
+    from ds_kernels import synthetic as syn
+    M = syn.moe_weights()
+    P = dm.DecoderLayerWeights.from_tensors(w, M, torch.device(DEV))
+    b, s = 1, 64
+    g = torch.Generator().manual_seed(13)
+    x = torch.randn(b, s, 2048, generator=g).to(torch.bfloat16)
+    cos, sin = dm.yarn_cos_sin(s)
+    out = dm.decoder_layer_forward(x.to(DEV), P, cos.to(DEV), sin.to(DEV))
+    p = {"in_norm": np.ones(2048, np.float32), "post_norm": np.ones(2048, np.float32),
+         "q": wn["q"], "kva": wn["kva"], "kva_norm": wn["kva_norm"], "kvb": wn["kvb"],
+         "o": wn["o"], "wg": _bf(M.wg), "gates": _bf(M.gates), "ups": _bf(M.ups),
+         "downs": _bf(M.downs), "shared": tuple(_bf(t) for t in M.shared)}
+    ref = ol.decoder_layer(np32(x), p)
+    assert out.shape == (b, s, 2048)
+    assert max_rel_err(np32(out), ref) <= BF16_TOL
