@@ -159,17 +159,28 @@ def bench_mla(dsk, syn, torch, ev, reps=20, warmup=5):
     k_pe = kva[..., 512:].view(b, s, 1, 64).transpose(1, 2)
     st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
 
-    def timed(fn):
+    def timed(fn, per_graph=10):
+        """Median time of fn on the GPU: per_graph back-to-back calls captured in
+        a HIP graph (so host-side Python cost between launches does not leave
+        the GPU idle), replayed `reps` times between HIP events on the stream."""
         for _ in range(warmup):
             fn()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(per_graph):
+                fn()
+        graph.replay()
+        torch.cuda.synchronize()
         evs = ev.create(2 * reps)
         for i in range(reps):
             ev.rt.hipEventRecord(evs[2 * i], st())
-            fn()
+            graph.replay()
             ev.rt.hipEventRecord(evs[2 * i + 1], st())
         torch.cuda.synchronize()
-        t = sorted(ev.ms(evs[2 * i], evs[2 * i + 1]) for i in range(reps))
+        t = sorted(ev.ms(evs[2 * i], evs[2 * i + 1]) / per_graph for i in range(reps))
         ev.destroy(evs)
+        del graph
         return t[len(t) // 2]
 
     rows = b * s
@@ -203,7 +214,7 @@ def bench_mla(dsk, syn, torch, ev, reps=20, warmup=5):
     P = dm.DecoderLayerWeights.from_tensors(syn.mla_weights(), syn.moe_weights(), dev)
     b4 = 4
     x4 = torch.randn(b4, s, H, generator=g).to(torch.bfloat16).to(dev)
-    t_layer = timed(lambda: dm.decoder_layer_forward(x4, P, cos, sin))
+    t_layer = timed(lambda: dm.decoder_layer_forward(x4, P, cos, sin), per_graph=2)
     out["config4_decoder_layer"] = {
         "shape": "b=4, s=2048, causal; MLA (16 heads) + MoE (64 routed top-6 + 2 shared)",
         "layer_ms": t_layer, "tokens_per_s": b4 * s / (t_layer * 1e-3)}

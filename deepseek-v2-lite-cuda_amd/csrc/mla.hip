@@ -63,44 +63,66 @@ __device__ __forceinline__ float to_f(float v) { return v; }
 __device__ __forceinline__ void from_f(float v, uint16_t* p) { *p = f32_to_bf16(v); }
 __device__ __forceinline__ void from_f(float v, float* p) { *p = v; }
 
-constexpr int kNormThreads = 256;  // 4 rows per workgroup
+constexpr int kNormThreads = 256;  // 4 waves per workgroup
 
 // NV = 8-element chunks held per lane in registers (H <= 512 * NV, H % 8 == 0).
-template <typename Tin, typename Tout, int NV>
+// Each wave normalises R rows: the weight vector and all R rows are loaded
+// before the first reduction, so a wave keeps R row loads in flight instead
+// of one (a 512-wide bf16 row is only 1 KB).
+template <typename Tin, typename Tout, int NV, int R>
 __global__ __launch_bounds__(kNormThreads) void rms_norm_vec_kernel(
     const Tin* __restrict__ in, int64_t ld_in, const float* __restrict__ w,
     Tout* __restrict__ out, int64_t ld_out, int rows, int H, float eps) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * (kNormThreads / 64) + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  const Tin* src = in + row * ld_in;
-  float x[NV][8];
-  float ss = 0.f;
+  const int64_t row0 = ((int64_t)blockIdx.x * (kNormThreads / 64) + (threadIdx.x >> 6)) * R;
+  if (row0 >= rows) return;
+  floatx4_t w0[NV], w1[NV];
+  float x[R][NV][8];
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int c = lane + 64 * j;
     if (c * 8 < H) {
-      Vec8<Tin>::load(src + c * 8, x[j]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ss = fmaf(x[j][e], x[j][e], ss);
+      w0[j] = *reinterpret_cast<const floatx4_t*>(w + c * 8);
+      w1[j] = *reinterpret_cast<const floatx4_t*>(w + c * 8 + 4);
     }
   }
-  ss = wave_sum(ss);
-  const float r = rsqrtf(ss / (float)H + eps);
-  Tout* dst = out + row * ld_out;
 #pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int c = lane + 64 * j;
-    if (c * 8 < H) {
-      const floatx4_t w0 = *reinterpret_cast<const floatx4_t*>(w + c * 8);
-      const floatx4_t w1 = *reinterpret_cast<const floatx4_t*>(w + c * 8 + 4);
-      float y[8];
+  for (int rr = 0; rr < R; ++rr) {
+    const int64_t row = min(row0 + rr, (int64_t)rows - 1);  // past the end: reload, unused
+    const Tin* src = in + row * ld_in;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        y[e] = (x[j][e] * r) * w0[e];
-        y[4 + e] = (x[j][4 + e] * r) * w1[e];
+    for (int j = 0; j < NV; ++j) {
+      const int c = lane + 64 * j;
+      if (c * 8 < H) Vec8<Tin>::load(src + c * 8, x[rr][j]);
+    }
+  }
+#pragma unroll
+  for (int rr = 0; rr < R; ++rr) {
+    if (row0 + rr >= rows) break;
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int c = lane + 64 * j;
+      if (c * 8 < H) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = fmaf(x[rr][j][e], x[rr][j][e], ss);
       }
-      Vec8<Tout>::store(dst + c * 8, y);
+    }
+    ss = wave_sum(ss);
+    const float r = rsqrtf(ss / (float)H + eps);
+    Tout* dst = out + (row0 + rr) * ld_out;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int c = lane + 64 * j;
+      if (c * 8 < H) {
+        float y[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          y[e] = (x[rr][j][e] * r) * w0[j][e];
+          y[4 + e] = (x[rr][j][4 + e] * r) * w1[j][e];
+        }
+        Vec8<Tout>::store(dst + c * 8, y);
+      }
     }
   }
 }
@@ -125,6 +147,23 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_scalar_kernel(
   for (int c = lane; c < H; c += 64) from_f((to_f(src[c]) * r) * w[c], dst + c);
 }
 
+// Rows per wave: enough row loads in flight at small H, while keeping at
+// least ~2 waves per SIMD of the chip busy for small row counts.
+template <typename Tin, typename Tout, int NV>
+static void launch_rms_norm_nv(const Tin* in, int64_t ld_in, const float* w, Tout* out,
+                               int64_t ld_out, int rows, int H, float eps, hipStream_t st) {
+  constexpr int R = NV == 1 ? 4 : (NV == 2 ? 2 : 1);
+  const int r = rows >= 2048 * R ? R : 1;
+  const int per_wg = (kNormThreads / 64) * r;
+  const unsigned grid = (unsigned)(((int64_t)rows + per_wg - 1) / per_wg);
+  if (r == R)
+    hipLaunchKernelGGL((rms_norm_vec_kernel<Tin, Tout, NV, R>), dim3(grid), dim3(kNormThreads),
+                       0, st, in, ld_in, w, out, ld_out, rows, H, eps);
+  else
+    hipLaunchKernelGGL((rms_norm_vec_kernel<Tin, Tout, NV, 1>), dim3(grid), dim3(kNormThreads),
+                       0, st, in, ld_in, w, out, ld_out, rows, H, eps);
+}
+
 template <typename Tin, typename Tout>
 static int launch_rms_norm(const Tin* in, int64_t ld_in, const float* w, Tout* out,
                            int64_t ld_out, int rows, int H, float eps, hipStream_t st) {
@@ -134,18 +173,10 @@ static int launch_rms_norm(const Tin* in, int64_t ld_in, const float* w, Tout* o
                    (ld_out * (int64_t)sizeof(Tout)) % 16 == 0;
   if (vec) {
     const int nv = (H + 511) / 512;
-    if (nv <= 1)
-      hipLaunchKernelGGL((rms_norm_vec_kernel<Tin, Tout, 1>), dim3(grid), dim3(kNormThreads), 0,
-                         st, in, ld_in, w, out, ld_out, rows, H, eps);
-    else if (nv <= 2)
-      hipLaunchKernelGGL((rms_norm_vec_kernel<Tin, Tout, 2>), dim3(grid), dim3(kNormThreads), 0,
-                         st, in, ld_in, w, out, ld_out, rows, H, eps);
-    else if (nv <= 4)
-      hipLaunchKernelGGL((rms_norm_vec_kernel<Tin, Tout, 4>), dim3(grid), dim3(kNormThreads), 0,
-                         st, in, ld_in, w, out, ld_out, rows, H, eps);
-    else
-      hipLaunchKernelGGL((rms_norm_vec_kernel<Tin, Tout, 8>), dim3(grid), dim3(kNormThreads), 0,
-                         st, in, ld_in, w, out, ld_out, rows, H, eps);
+    if (nv <= 1) launch_rms_norm_nv<Tin, Tout, 1>(in, ld_in, w, out, ld_out, rows, H, eps, st);
+    else if (nv <= 2) launch_rms_norm_nv<Tin, Tout, 2>(in, ld_in, w, out, ld_out, rows, H, eps, st);
+    else if (nv <= 4) launch_rms_norm_nv<Tin, Tout, 4>(in, ld_in, w, out, ld_out, rows, H, eps, st);
+    else launch_rms_norm_nv<Tin, Tout, 8>(in, ld_in, w, out, ld_out, rows, H, eps, st);
   } else {
     hipLaunchKernelGGL((rms_norm_scalar_kernel<Tin, Tout>), dim3(grid), dim3(kNormThreads), 0,
                        st, in, ld_in, w, out, ld_out, rows, H, eps);
@@ -163,53 +194,54 @@ struct RopeTensor {
   int heads;
 };
 
-__global__ __launch_bounds__(256) void rope_kernel(RopeTensor a, RopeTensor b, int64_t rows_a,
-                                                   int64_t rows_b,
+// One thread per 8 elements (4 pairs) with 32-bit index arithmetic (a 64-bit
+// division per element would cost more than the memory traffic).
+__global__ __launch_bounds__(256) void rope_kernel(RopeTensor a, RopeTensor b, int items_a,
+                                                   int items_b,
                                                    const uint16_t* __restrict__ cos_t,
                                                    const uint16_t* __restrict__ sin_t,
                                                    int64_t cb, int64_t cs, int S, int d) {
-  const int cpr = d / 8;
-  const int half = d / 2;
-  const int64_t total = (rows_a + rows_b) * cpr;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    int64_t row = i / cpr;
-    const int c = (int)(i - row * cpr);
-    const RopeTensor& r = row < rows_a ? a : b;
-    if (row >= rows_a) row -= rows_a;
-    const int s = (int)(row % S);
-    const int64_t bh = row / S;
-    const int h = (int)(bh % r.heads);
-    const int bb = (int)(bh / r.heads);
-    const uint16_t* xp = r.x + bb * r.sb + h * r.sh + (int64_t)s * r.ss + c * 8;
-    const int64_t toff = bb * cb + (int64_t)s * cs;
-    const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(xp);
-    const u32x2_t clo = *reinterpret_cast<const u32x2_t*>(cos_t + toff + 4 * c);
-    const u32x2_t chi = *reinterpret_cast<const u32x2_t*>(cos_t + toff + half + 4 * c);
-    const u32x2_t slo = *reinterpret_cast<const u32x2_t*>(sin_t + toff + 4 * c);
-    const u32x2_t shi = *reinterpret_cast<const u32x2_t*>(sin_t + toff + half + 4 * c);
-    float lo[4], hi[4];
+  int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= items_a + items_b) return;
+  const bool is_a = i < items_a;
+  const RopeTensor& r = is_a ? a : b;
+  if (!is_a) i -= items_a;
+  const int cpr = d >> 3;
+  const int half = d >> 1;
+  const int row = i / cpr;               // output row = (bb * heads + h) * S + s
+  const int c = i - row * cpr;
+  const int bh = row / S;
+  const int s = row - bh * S;
+  const int bb = bh / r.heads;
+  const int h = bh - bb * r.heads;
+  const uint16_t* xp = r.x + bb * r.sb + h * r.sh + (int64_t)s * r.ss + c * 8;
+  const int64_t toff = bb * cb + (int64_t)s * cs;
+  const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(xp);
+  const u32x2_t clo = *reinterpret_cast<const u32x2_t*>(cos_t + toff + 4 * c);
+  const u32x2_t chi = *reinterpret_cast<const u32x2_t*>(cos_t + toff + half + 4 * c);
+  const u32x2_t slo = *reinterpret_cast<const u32x2_t*>(sin_t + toff + 4 * c);
+  const u32x2_t shi = *reinterpret_cast<const u32x2_t*>(sin_t + toff + half + 4 * c);
+  float lo[4], hi[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float x0 = bf16lo(xv[j]);  // x[2k]
-      const float x1 = bf16hi(xv[j]);  // x[2k+1]
-      const uint32_t cl = clo[j >> 1], ch = chi[j >> 1], sl = slo[j >> 1], sh = shi[j >> 1];
-      const float c_lo = (j & 1) ? bf16hi(cl) : bf16lo(cl);
-      const float c_hi = (j & 1) ? bf16hi(ch) : bf16lo(ch);
-      const float s_lo = (j & 1) ? bf16hi(sl) : bf16lo(sl);
-      const float s_hi = (j & 1) ? bf16hi(sh) : bf16lo(sh);
-      lo[j] = x0 * c_lo - x1 * s_lo;
-      hi[j] = x1 * c_hi + x0 * s_hi;
-    }
-    uint16_t* op = r.out + row * d;
-    u32x2_t olo, ohi;
-    olo[0] = pack_bf16x2(lo[0], lo[1]);
-    olo[1] = pack_bf16x2(lo[2], lo[3]);
-    ohi[0] = pack_bf16x2(hi[0], hi[1]);
-    ohi[1] = pack_bf16x2(hi[2], hi[3]);
-    *reinterpret_cast<u32x2_t*>(op + 4 * c) = olo;
-    *reinterpret_cast<u32x2_t*>(op + half + 4 * c) = ohi;
+  for (int j = 0; j < 4; ++j) {
+    const float x0 = bf16lo(xv[j]);  // x[2k]
+    const float x1 = bf16hi(xv[j]);  // x[2k+1]
+    const uint32_t cl = clo[j >> 1], ch = chi[j >> 1], sl = slo[j >> 1], sh = shi[j >> 1];
+    const float c_lo = (j & 1) ? bf16hi(cl) : bf16lo(cl);
+    const float c_hi = (j & 1) ? bf16hi(ch) : bf16lo(ch);
+    const float s_lo = (j & 1) ? bf16hi(sl) : bf16lo(sl);
+    const float s_hi = (j & 1) ? bf16hi(sh) : bf16lo(sh);
+    lo[j] = x0 * c_lo - x1 * s_lo;
+    hi[j] = x1 * c_hi + x0 * s_hi;
   }
+  uint16_t* op = r.out + (int64_t)row * d;
+  u32x2_t olo, ohi;
+  olo[0] = pack_bf16x2(lo[0], lo[1]);
+  olo[1] = pack_bf16x2(lo[2], lo[3]);
+  ohi[0] = pack_bf16x2(hi[0], hi[1]);
+  ohi[1] = pack_bf16x2(hi[2], hi[3]);
+  *reinterpret_cast<u32x2_t*>(op + 4 * c) = olo;
+  *reinterpret_cast<u32x2_t*>(op + half + 4 * c) = ohi;
 }
 
 static int check_rope(const void* x, int64_t sb, int64_t sh, int64_t ss, const void* out,
@@ -270,12 +302,14 @@ extern "C" int dsk_rope_qk(const dsk_bf16* q, int64_t qsb, int64_t qsh, int64_t 
   int rc;
   if (rows_q && (rc = check_rope(q, qsb, qsh, qss, q_out, d))) return rc;
   if (rows_k && (rc = check_rope(k, ksb, ksh, kss, k_out, d))) return rc;
+  DSK_REQUIRE((rows_q + rows_k) * (d / 8) < (int64_t)INT32_MAX, DSK_ERR_INVALID_ARG,
+              "rope: more than 2^31 8-element chunks");
   RopeTensor a{q, qsb, qsh, qss, q_out, Hq > 0 ? Hq : 1};
   RopeTensor b{k, ksb, ksh, kss, k_out, Hk > 0 ? Hk : 1};
-  const int64_t work = (rows_q + rows_k) * (d / 8);
-  const unsigned grid = (unsigned)std::min<int64_t>((work + 255) / 256, 16384);
-  hipLaunchKernelGGL(rope_kernel, dim3(grid), dim3(256), 0, as_stream(stream), a, b, rows_q,
-                     rows_k, cos_t, sin_t, cb, cs, S, d);
+  const int items_q = (int)(rows_q * (d / 8)), items_k = (int)(rows_k * (d / 8));
+  const unsigned grid = (unsigned)(((int64_t)items_q + items_k + 255) / 256);
+  hipLaunchKernelGGL(rope_kernel, dim3(grid), dim3(256), 0, as_stream(stream), a, b, items_q,
+                     items_k, cos_t, sin_t, cb, cs, S, d);
   return check_launch("rope_kernel");
 }
 

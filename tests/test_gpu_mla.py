@@ -19,7 +19,7 @@ def dsk():
 
 
 @pytest.mark.parametrize("rows,H", [(4, 512), (64, 512), (1000, 512), (33, 2048), (8, 6),
-                                    (5, 4096), (3, 5000)])
+                                    (5, 4096), (3, 5000), (20001, 512), (9001, 1024)])
 def test_rms_norm_bf16(dsk, rows, H):
     g = torch.Generator().manual_seed(rows + H)
     x = (torch.randn(rows, H, generator=g) * 0.5).to(torch.bfloat16)
