@@ -165,9 +165,13 @@ struct GemmCfg {
   static constexpr int OUT_N = SWIGLU ? BN / 2 : BN;
   static constexpr int CPR = BK / 8;        // 16-byte chunks per LDS row
   static constexpr int RPI = 64 / CPR;      // rows per 1 KB DMA instruction
-  static constexpr int A_INSTS = BM / (NW * RPI);  // DMA instructions per wave per stage
-  static constexpr int B_INSTS = BN / (NW * RPI);
-  static_assert(A_INSTS * NW * RPI == BM && B_INSTS * NW * RPI == BN, "tile rows vs DMA rows");
+  // DMA is issued by the first NI waves only, one per SIMD: a wave stalls
+  // while the address unit drains its DMA instructions, and the second wave
+  // on the SIMD keeps the matrix core busy meanwhile.
+  static constexpr int NI = 4;
+  static constexpr int A_INSTS = BM / (NI * RPI);  // DMA instructions per issuing wave per stage
+  static constexpr int B_INSTS = BN / (NI * RPI);
+  static_assert(A_INSTS * NI * RPI == BM && B_INSTS * NI * RPI == BN, "tile rows vs DMA rows");
   static constexpr int KSTEPS = BK / 16;
   static constexpr int A_BYTES = BM * BK * 2;
   static constexpr int STAGE_BYTES = (BM + BN) * BK * 2;
@@ -195,7 +199,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void grouped_gemm_kernel
   constexpr int OUT_N = Cfg::OUT_N;
   constexpr int CPR = Cfg::CPR, RPI = Cfg::RPI;
   constexpr int A_INSTS = Cfg::A_INSTS, B_INSTS = Cfg::B_INSTS;
-  constexpr int NL = A_INSTS + B_INSTS;  // DMA instructions per thread per stage
+  constexpr int NL = A_INSTS + B_INSTS;  // DMA instructions per issuing wave per stage
+  constexpr int NI = Cfg::NI;
   constexpr int KSTEPS = Cfg::KSTEPS;
   constexpr int NW = Cfg::NW;
 
@@ -309,13 +314,18 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void grouped_gemm_kernel
     __syncthreads();
   }
 
-  // ---- issue side of the stage stream
-  const uint16_t* a_src[A_INSTS];
-  const uint16_t* b_src[B_INSTS];
+  // ---- issue side of the stage stream (waves 0 .. NI-1). Sources are kept
+  // as 32-bit byte offsets from uniform bases (A, and the tile's weight group),
+  // one VGPR each.
+  const bool issuer = wave < NI;
+  uint32_t a_off[A_INSTS], b_off[B_INSTS];
+  const char* Bg = reinterpret_cast<const char*>(p.B);
   auto set_sources = [&](int t_idx, const Tile& t) {
+    Bg = reinterpret_cast<const char*>(p.B + (int64_t)t.g * p.b_group_stride);
+    if (!issuer) return;
 #pragma unroll
     for (int i = 0; i < A_INSTS; ++i) {
-      const int r = RPI * (wave + NW * i) + dma_row;
+      const int r = RPI * (wave + NI * i) + dma_row;
       int row;
       if constexpr (GATHER) {
         row = s_rows[t_idx * BM + r];
@@ -324,15 +334,14 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void grouped_gemm_kernel
         row = m < t.me ? m : t.m0;
       }
       row = (row >= 0 && row < row_limit) ? row : 0;
-      a_src[i] = p.A + (int64_t)row * p.lda + dma_chunk * 8;
+      a_off[i] = (uint32_t)(((int64_t)row * p.lda + dma_chunk * 8) * 2);
     }
-    const uint16_t* Bg = p.B + (int64_t)t.g * p.b_group_stride;
 #pragma unroll
     for (int i = 0; i < B_INSTS; ++i) {
       if constexpr (TILED) {
         // one 1 KB fragment (32 weight rows x 16 k) per instruction: local
         // fragment f = row block * (BK/16) + k step
-        const int f = wave + NW * i;
+        const int f = wave + NI * i;
         const int rbl = f / (BK / 16), ksl = f % (BK / 16);
         int rb;
         if constexpr (SWIGLU) {
@@ -342,9 +351,9 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void grouped_gemm_kernel
         } else {
           rb = min(t.n0 / 32 + rbl, p.N / 32 - 1);
         }
-        b_src[i] = Bg + ((int64_t)rb * (p.K / 16) + ksl) * 512 + lane * 8;
+        b_off[i] = (uint32_t)((((int64_t)rb * (p.K / 16) + ksl) * 512 + lane * 8) * 2);
       } else {
-        const int r = RPI * (wave + NW * i) + dma_row;
+        const int r = RPI * (wave + NI * i) + dma_row;
         int brow, col;
         if constexpr (SWIGLU) {
           const int wn = r / WN, w = r % WN;
@@ -355,25 +364,27 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void grouped_gemm_kernel
           col = min(t.n0 + r, p.N - 1);
           brow = col;
         }
-        b_src[i] = Bg + (int64_t)brow * p.ldb + dma_chunk * 8;
+        b_off[i] = (uint32_t)(((int64_t)brow * p.ldb + dma_chunk * 8) * 2);
       }
     }
   };
   auto issue = [&](int stage, int kt) {
-    const int koff = kt * BK;
-    // tiled weights: a stage is BK/16 consecutive fragments of 512 elements
-    const int bkoff = TILED ? kt * (BK / 16) * 512 : koff;
+    if (!issuer) return;
+    const uint32_t koff = (uint32_t)kt * BK * 2;  // bytes
+    // tiled weights: a stage is BK/16 consecutive fragments of 1 KB
+    const uint32_t bkoff = TILED ? (uint32_t)kt * (BK / 16) * 1024 : koff;
     const uint32_t sbase = lds_base + stage * Cfg::STAGE_BYTES;
+    const char* A = reinterpret_cast<const char*>(p.A);
 #pragma unroll
     for (int i = 0; i < A_INSTS; ++i) {
-      const uint32_t dst = sbase + (wave + NW * i) * 1024;
-      __builtin_amdgcn_global_load_lds((global_void_t*)(a_src[i] + koff),
+      const uint32_t dst = sbase + (wave + NI * i) * 1024;
+      __builtin_amdgcn_global_load_lds((global_void_t*)(A + (a_off[i] + koff)),
                                        (lds_void_t*)(uintptr_t)dst, 16, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < B_INSTS; ++i) {
-      const uint32_t dst = sbase + Cfg::A_BYTES + (wave + NW * i) * 1024;
-      __builtin_amdgcn_global_load_lds((global_void_t*)(b_src[i] + bkoff),
+      const uint32_t dst = sbase + Cfg::A_BYTES + (wave + NI * i) * 1024;
+      __builtin_amdgcn_global_load_lds((global_void_t*)(Bg + (b_off[i] + bkoff)),
                                        (lds_void_t*)(uintptr_t)dst, 16, 0, 0);
     }
   };
