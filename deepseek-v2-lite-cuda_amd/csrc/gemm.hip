@@ -165,9 +165,11 @@ struct GemmCfg {
   static constexpr int OUT_N = SWIGLU ? BN / 2 : BN;
   static constexpr int CPR = BK / 8;        // 16-byte chunks per LDS row
   static constexpr int RPI = 64 / CPR;      // rows per 1 KB DMA instruction
-  // DMA is issued by the first NI waves only, one per SIMD: a wave stalls
-  // while the address unit drains its DMA instructions, and the second wave
-  // on the SIMD keeps the matrix core busy meanwhile.
+  // DMA is issued by NI waves only, one per SIMD: a wave stalls while the
+  // address unit drains its DMA instructions, and the second wave on the SIMD
+  // keeps the matrix core busy meanwhile. The issuers are the last NI waves
+  // (the highest wave_m): a partial M tile fills the first waves' rows first,
+  // so the issuing waves have the fewest MFMAs.
   static constexpr int NI = 4;
   static constexpr int A_INSTS = BM / (NI * RPI);  // DMA instructions per issuing wave per stage
   static constexpr int B_INSTS = BN / (NI * RPI);
@@ -289,10 +291,11 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void grouped_gemm_kernel
   };
 
   // DMA lane mapping: lane l lands at row l / CPR of its instruction's row group
-  // (RPI rows; group index wave + 4i), physical chunk l % CPR
+  // (RPI rows; group index islot + NI*i), physical chunk l % CPR
+  const int islot = wave - (NW - NI);  // issuing slot 0 .. NI-1, negative if not issuing
   const int dma_row = lane / CPR;
   int dma_chunk;
-  if constexpr (CPR == 8) dma_chunk = (lane & 7) ^ dma_row ^ (wave & 1);
+  if constexpr (CPR == 8) dma_chunk = (lane & 7) ^ dma_row ^ (islot & 1);
   else dma_chunk = (lane & 3) ^ ((lane >> 4) & 3);
   const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
   const u32x4_t* lds4 = reinterpret_cast<const u32x4_t*>(lds);
@@ -317,7 +320,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void grouped_gemm_kernel
   // ---- issue side of the stage stream (waves 0 .. NI-1). Sources are kept
   // as 32-bit byte offsets from uniform bases (A, and the tile's weight group),
   // one VGPR each.
-  const bool issuer = wave < NI;
+  const bool issuer = islot >= 0;
   uint32_t a_off[A_INSTS], b_off[B_INSTS];
   const char* Bg = reinterpret_cast<const char*>(p.B);
   auto set_sources = [&](int t_idx, const Tile& t) {
@@ -325,7 +328,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void grouped_gemm_kernel
     if (!issuer) return;
 #pragma unroll
     for (int i = 0; i < A_INSTS; ++i) {
-      const int r = RPI * (wave + NI * i) + dma_row;
+      const int r = RPI * (islot + NI * i) + dma_row;
       int row;
       if constexpr (GATHER) {
         row = s_rows[t_idx * BM + r];
@@ -341,7 +344,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void grouped_gemm_kernel
       if constexpr (TILED) {
         // one 1 KB fragment (32 weight rows x 16 k) per instruction: local
         // fragment f = row block * (BK/16) + k step
-        const int f = wave + NI * i;
+        const int f = islot + NI * i;
         const int rbl = f / (BK / 16), ksl = f % (BK / 16);
         int rb;
         if constexpr (SWIGLU) {
@@ -353,7 +356,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void grouped_gemm_kernel
         }
         b_off[i] = (uint32_t)((((int64_t)rb * (p.K / 16) + ksl) * 512 + lane * 8) * 2);
       } else {
-        const int r = RPI * (wave + NI * i) + dma_row;
+        const int r = RPI * (islot + NI * i) + dma_row;
         int brow, col;
         if constexpr (SWIGLU) {
           const int wn = r / WN, w = r % WN;
@@ -377,13 +380,13 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void grouped_gemm_kernel
     const char* A = reinterpret_cast<const char*>(p.A);
 #pragma unroll
     for (int i = 0; i < A_INSTS; ++i) {
-      const uint32_t dst = sbase + (wave + NI * i) * 1024;
+      const uint32_t dst = sbase + (islot + NI * i) * 1024;
       __builtin_amdgcn_global_load_lds((global_void_t*)(A + (a_off[i] + koff)),
                                        (lds_void_t*)(uintptr_t)dst, 16, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < B_INSTS; ++i) {
-      const uint32_t dst = sbase + Cfg::A_BYTES + (wave + NI * i) * 1024;
+      const uint32_t dst = sbase + Cfg::A_BYTES + (islot + NI * i) * 1024;
       __builtin_amdgcn_global_load_lds((global_void_t*)(Bg + (b_off[i] + bkoff)),
                                        (lds_void_t*)(uintptr_t)dst, 16, 0, 0);
     }
