@@ -15,10 +15,13 @@ Also reported on the same line:
                 GB/s of algorithmic bytes (touched expert weights + shared + gate +
                 activations) per layer step, weights rotated over 4 copies so the
                 256 MB MALL cannot serve them.
+  mla           BASELINE configs 3 and 4: the MLA projection block (rms_norm on the
+                strided latent, rope, kv_upproj, each timed by HIP-graph replay) and
+                the decoder layer, composed from this library's kernels.
   cpu_baseline  the CPU oracle (numpy restatement of DeepSeekMoE.forward) timed
                 on a bounded sample (config 0, T=64 fp32) on this host's cores.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--profile | --decode-only T]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--profile | --decode-only T | --mla-only]
 """
 from __future__ import annotations
 
@@ -316,6 +319,8 @@ def main():
                     help="only the decode-shaped layer at T tokens (for profiling)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only the 1 GiB device copy used to scale the HBM counters")
+    ap.add_argument("--mla-only", action="store_true",
+                    help="only the MLA projection block and decoder layer (for profiling)")
     args = ap.parse_args()
     if args.calibrate_copy:
         calibrate_copy(3)
@@ -333,6 +338,9 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.mla_only:
+        print(json.dumps(bench_mla(dsk, syn, torch, HipEvents())), flush=True)
+        return
     print("bench: generating synthetic weights", file=sys.stderr, flush=True)
     W = syn.moe_weights()
     w1, w2, nsh = dsk.pack_tensors(W.gates, W.ups, W.downs, device=dev, shared=W.shared)

@@ -114,18 +114,21 @@ def mla_projections(x: torch.Tensor, W: MLAWeights, cos: torch.Tensor, sin: torc
 def mla_forward(x: torch.Tensor, W: MLAWeights, cos: torch.Tensor, sin: torch.Tensor,
                 eps: float = 1e-6) -> torch.Tensor:
     """DeepSeekMLA.forward (mla.py:295-393) for positions 0..s-1 with the causal
-    mask: projections on this package's kernels, attention core in fp32 torch,
-    o_proj on the MFMA GEMM. x: bf16 [b, s, H] -> bf16 [b, s, H]."""
+    mask: projections on this package's kernels, o_proj on the MFMA GEMM, and
+    the attention core in torch at the reference's precision (mla.py:366-384):
+    bf16 Q.K^T, scale, causal mask, softmax in fp32 rounded to bf16, bf16 .V.
+    The right-hand operands are made contiguous before the batched products.
+    x: bf16 [b, s, H] -> bf16 [b, s, H]."""
     b, s, H = x.shape
     q_nope, q_rot, k_nope, v, k_rot, _ = mla_projections(x, W, cos, sin, eps)
-    q = torch.cat([q_nope, q_rot], dim=-1).float()
-    k = torch.cat([k_nope, k_rot.expand(b, W.n_heads, s, W.rope_dim)], dim=-1).float()
+    q = torch.cat([q_nope, q_rot], dim=-1)                             # [b,h,s,192]
+    k = torch.cat([k_nope, k_rot.expand(b, W.n_heads, s, W.rope_dim)], dim=-1)
     scores = torch.matmul(q, k.transpose(-1, -2).contiguous()) * W.softmax_scale
     causal = torch.ones(s, s, dtype=torch.bool, device=x.device).triu(1)
     scores.masked_fill_(causal, float("-inf"))
-    p = torch.softmax(scores, dim=-1)
-    o = torch.matmul(p, v.float().contiguous())                        # [b,h,s,v]
-    o = o.transpose(1, 2).reshape(b, s, W.n_heads * W.v_dim).to(torch.bfloat16)
+    p = torch.softmax(scores, dim=-1, dtype=torch.float32).to(torch.bfloat16)
+    o = torch.matmul(p, v.contiguous())                                # [b,h,s,v]
+    o = o.transpose(1, 2).reshape(b, s, W.n_heads * W.v_dim)
     return ops.linear(o, W.o)
 
 
