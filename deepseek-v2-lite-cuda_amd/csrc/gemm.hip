@@ -551,6 +551,384 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void grouped_gemm_kernel
   }
 }
 
+// ------------------------------------------- large groups, tiled weights ----
+// Grouped GEMM for fragment-tiled weights, one wave per SIMD. A tile is 256
+// token rows x 256 weight rows; each of the 4 waves owns 64 weight rows (two
+// 32-row fragments) against all 256 token rows: 8 x 2 blocks of 32 x 32, 256
+// fp32 accumulators per lane in the accumulator registers.
+//   * Weights go straight from HBM/L2 into registers, two stages (128 K)
+//     ahead of their use: a wave's weight rows belong to it alone, and a
+//     tiled fragment is one contiguous 1 KB load in MFMA lane order.
+//   * Only the token rows go through the LDS: a 4-deep ring of 32 KB stages
+//     (256 rows x 64 K) filled by direct global->LDS DMA three stages ahead,
+//     read back as 8 fragments per K step by every wave.
+//   * Every memory operation of a stage (8 weight loads, 8 DMA instructions
+//     per wave) is spread over the stage's MFMAs, so no wave stalls on a burst
+//     of issue and the matrix core of each SIMD is fed by a single wave.
+//   * One workgroup barrier per stage; all 4 waves do the same work, so no
+//     wave waits for another's extra MFMAs.
+// The issue cursors (tokens three stages ahead, weights two) run over the
+// tile stream of the workgroup, so the next tile's first stages are in flight
+// during the epilogue. Past the end of the stream they repeat the last valid
+// stage (into a ring slot and registers nobody reads again), which keeps the
+// number of memory operations per stage fixed for the vmcnt bookkeeping.
+constexpr int kWideWaves = 4;
+constexpr int kWideBM = 256;                           // token rows per tile
+constexpr int kWideBK = 64;                            // K per stage
+constexpr int kWideRing = 4;                           // token stages in the LDS ring
+constexpr int kWideStageBytes = kWideBM * kWideBK * 2;  // 32 KB
+constexpr int kWideRingBytes = kWideRing * kWideStageBytes;
+constexpr int kWideRowTiles = (kLdsPerCU - kWideRingBytes - 4096) / (kWideBM * 4);
+constexpr int kWideLdsBytes = kWideRingBytes + kWideRowTiles * kWideBM * 4;
+
+// Global->LDS DMA of 16 bytes per lane (1 KB per wave to lds_addr) from
+// base + voff, as inline asm. The compiler's wait-count bookkeeping does not
+// model this LDS-writing load alongside ordinary register loads (with both in
+// flight it falls back to waiting for every outstanding load before each use);
+// hidden from it, the register loads keep exact counts, which can only be
+// stricter than needed since this DMA is not counted. The "memory" clobber
+// keeps every other memory access in program order around it; completion is
+// waited for explicitly (wait_vmcnt) before the workgroup barrier.
+__device__ __forceinline__ void dma_1kb(const char* base, uint32_t voff, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(base), "s"(lds_addr) : "memory", "m0");
+}
+
+template <bool SWIGLU, bool GATHER>
+__global__ __launch_bounds__(64 * kWideWaves, 1) void wide_gemm_kernel(GemmArgs p) {
+  constexpr int TM = kWideBM / 32;     // token blocks per tile
+  constexpr int TN = 2;                // weight blocks per wave
+  constexpr int KSTEPS = kWideBK / 16;
+  constexpr int OUT_N = SWIGLU ? 32 * kWideWaves : 64 * kWideWaves;  // output columns per tile
+  constexpr int RPI = 8;               // token rows per 1 KB DMA instruction
+  constexpr int A_INSTS = kWideBM / (kWideWaves * RPI);  // per wave per stage
+  static_assert(A_INSTS == 2 * KSTEPS, "two DMA instructions per K step");
+  constexpr int THREADS = 64 * kWideWaves;
+
+  extern __shared__ __attribute__((aligned(1024))) uint16_t lds[];
+  __shared__ int s_inc[kMaxGroups];
+  __shared__ int s_mb[kMaxGroups];
+  __shared__ int s_me[kMaxGroups];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int G = p.offsets != nullptr ? p.G : 1;
+  const int NT = (p.N + OUT_N - 1) / OUT_N;
+
+  // ---- group table (as in grouped_gemm_kernel): row ranges, even M split
+  if (tid < kMaxGroups) {
+    int cnt = 0;
+    if (tid < G) {
+      int mb = 0, me = p.M;
+      if (p.offsets != nullptr) {
+        mb = min(max(p.offsets[tid], 0), p.M);
+        me = min(max(p.offsets[tid + 1], mb), p.M);
+      }
+      s_mb[tid] = mb;
+      s_me[tid] = me;
+      cnt = ((me - mb + kWideBM - 1) / kWideBM) * NT;
+    }
+    s_inc[tid] = wave_inclusive_scan(cnt);
+  }
+  __syncthreads();
+  const int carry = s_inc[63];
+  __syncthreads();
+  if (tid >= 64 && tid < kMaxGroups) s_inc[tid] += carry;
+  __syncthreads();
+  const int total_tiles = s_inc[G - 1];
+
+  // ---- XCD-aware persistent enumeration (as in grouped_gemm_kernel)
+  constexpr int kChunk = kTileChunk;
+  const int xcd = blockIdx.x & 7;
+  const int slot = blockIdx.x >> 3;
+  const int per_xcd = gridDim.x >> 3;
+  const int n_chunks = (total_tiles + kChunk - 1) / kChunk;
+  int xcd_tiles = 0;
+  if (xcd < n_chunks) {
+    const int mine = (n_chunks - xcd + 7) >> 3;
+    xcd_tiles = mine * kChunk;
+    if ((n_chunks - 1) % 8 == xcd) xcd_tiles -= n_chunks * kChunk - total_tiles;
+  }
+  if (slot >= xcd_tiles) return;
+  const int ntiles = (xcd_tiles - slot + per_xcd - 1) / per_xcd;
+  const int nk = p.K / kWideBK;  // even (K % 128 == 0, checked by the launcher)
+  const int total = ntiles * nk;
+
+  struct Tile {
+    int g, m0, me, n0;
+  };
+  auto decode = [&](int t) -> Tile {
+    const int q = slot + t * per_xcd;
+    const int W = ((q / kChunk) * 8 + xcd) * kChunk + q % kChunk;
+    int lo = 0, hi = G - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (s_inc[mid] > W) hi = mid; else lo = mid + 1;
+    }
+    const int local = W - (lo > 0 ? s_inc[lo - 1] : 0);
+    const int mb = s_mb[lo], gme = s_me[lo];
+    const int mt = (gme - mb + kWideBM - 1) / kWideBM;
+    const int nblk = (gme - mb + 31) / 32;
+    const int nt = local / mt;
+    const int mi = local - nt * mt;
+    const int m0 = mb + 32 * (mi * nblk / mt);
+    const int me = min(mb + 32 * ((mi + 1) * nblk / mt), gme);
+    return Tile{lo, m0, me, nt * OUT_N};
+  };
+
+  const int dma_row = lane >> 3;
+  const int dma_chunk = (lane & 7) ^ dma_row ^ (wave & 1);  // row group wave + 4i: parity wave
+  const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
+  const u32x4_t* lds4 = reinterpret_cast<const u32x4_t*>(lds);
+  const int row_limit = GATHER ? p.a_rows_limit : p.M;
+
+  int* s_rows = reinterpret_cast<int*>(lds + kWideRingBytes / 2);
+  if constexpr (GATHER) {
+    if (ntiles > kWideRowTiles) return;  // excluded by the launcher
+    for (int idx = tid; idx < ntiles * kWideBM; idx += THREADS) {
+      const Tile t = decode(idx / kWideBM);
+      const int m = t.m0 + idx % kWideBM;
+      s_rows[idx] = p.a_rows[m < t.me ? m : t.m0];
+    }
+    __syncthreads();
+  }
+
+  // ---- token DMA cursor (three stages ahead of consumption)
+  const char* Abase = reinterpret_cast<const char*>(p.A);
+  uint32_t a_off[A_INSTS];
+  int a_gs = 0, a_tile = 0, a_kt = 0;
+  auto set_a = [&](int t_idx) {
+    const Tile t = decode(t_idx);
+#pragma unroll
+    for (int i = 0; i < A_INSTS; ++i) {
+      const int r = RPI * (wave + kWideWaves * i) + dma_row;
+      int row;
+      if constexpr (GATHER) {
+        row = s_rows[t_idx * kWideBM + r];
+      } else {
+        const int m = t.m0 + r;
+        row = m < t.me ? m : t.m0;
+      }
+      row = (row >= 0 && row < row_limit) ? row : 0;
+      a_off[i] = (uint32_t)(((int64_t)row * p.lda + dma_chunk * 8) * 2);
+    }
+  };
+  // DMA instructions i0, i0+1 of stage a_gs (ring slot a_gs % kWideRing)
+  auto issue_a = [&](int i0) {
+    const uint32_t koff = (uint32_t)a_kt * kWideBK * 2;
+    const uint32_t dst = lds_base + (a_gs % kWideRing) * kWideStageBytes;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int i = i0 + u;
+      dma_1kb(Abase, a_off[i] + koff, dst + (wave + kWideWaves * i) * 1024);
+    }
+  };
+  auto advance_a = [&]() {
+    ++a_gs;
+    if (a_gs < total && ++a_kt == nk) {
+      a_kt = 0;
+      set_a(++a_tile);
+    }
+  };
+
+  // ---- weight cursor (two stages ahead): fragment (rb, k step) of the tile's
+  // group at byte ((rb * K/16 + ks) * 512 + lane * 8) * 2
+  const char* b_grp = reinterpret_cast<const char*>(p.B);
+  uint32_t b_off[TN];
+  int b_gs = 0, b_tile = 0, b_kt = 0;
+  auto set_b = [&](int t_idx) {
+    const Tile t = decode(t_idx);
+    b_grp = reinterpret_cast<const char*>(p.B + (int64_t)t.g * p.b_group_stride);
+    const int last = p.N / 32 - 1;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      int rb;
+      if constexpr (SWIGLU) {
+        const int ob = min(t.n0 / 32 + wave, last);   // output block of this wave
+        rb = j == 0 ? ob : p.up_row_offset / 32 + ob;  // gate rows, then up rows
+      } else {
+        rb = min(t.n0 / 32 + TN * wave + j, last);
+      }
+      b_off[j] = (uint32_t)((((int64_t)rb * (p.K / 16)) * 512 + lane * 8) * 2);
+    }
+  };
+  auto issue_b = [&](bf16x8_t (&dst)[TN], int k) {
+    const uint32_t koff = (uint32_t)(b_kt * KSTEPS + k) * 1024;
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      dst[j] = *reinterpret_cast<const bf16x8_t*>(b_grp + (b_off[j] + koff));
+  };
+  auto advance_b = [&]() {
+    ++b_gs;
+    if (b_gs < total && ++b_kt == nk) {
+      b_kt = 0;
+      set_b(++b_tile);
+    }
+  };
+
+  bf16x8_t fb[2][KSTEPS][TN];  // weight fragments, register set = stage parity
+  bf16x8_t fa[2][TM];          // token fragments, double-buffered by K step
+  floatx16_t acc[TN][TM];
+#pragma unroll
+  for (int j = 0; j < TN; ++j)
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.f;
+
+  auto read_a = [&](bf16x8_t (&dst)[TM], int slot_idx, int kk) {
+    const u32x4_t* As = lds4 + slot_idx * (kWideStageBytes / 16);
+    const int ch = 2 * kk + (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+      dst[i] = __builtin_bit_cast(bf16x8_t, As[lds_swz<8>(32 * i + (lane & 31), ch)]);
+  };
+
+  // ---- prologue: tokens of stages 0-2 and weights of stages 0-1 in flight
+  // (order A0 B0 A1 B1 A2: 40 operations per wave), stage 0 landed
+  set_a(0);
+  set_b(0);
+#pragma unroll
+  for (int s = 0; s < 3; ++s) {
+#pragma unroll
+    for (int i = 0; i < A_INSTS; i += 2) issue_a(i);
+    advance_a();
+    if (s < 2) {
+#pragma unroll
+      for (int k = 0; k < KSTEPS; ++k) issue_b(fb[s][k], k);
+      advance_b();
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  wait_vmcnt<4 * A_INSTS>();  // everything after A0 may be pending
+  lds_barrier();
+  read_a(fa[0], 0, 0);
+
+  int gc = 0;  // stages consumed
+  Tile ct = decode(0);
+#pragma unroll 1
+  for (int ct_idx = 0; ct_idx < ntiles; ++ct_idx) {
+    // active 32-row token blocks of this tile (uniform). Blocks 0..TM/2-1 are
+    // always computed (rows past the tile end are never stored); the others
+    // sit behind uniform branches. A copy of the K loop per block count would
+    // merge 256 live accumulators at the branch and overflow the registers.
+    const int tma = max(1, min(TM, (ct.me - ct.m0 + 31) / 32));
+    {
+      // one stage: K steps 0..3 on weight set SET; the barrier before the last
+      // step publishes the next stage's tokens and frees this stage's slot
+      auto stage = [&](auto set_c) {
+        constexpr int SET = decltype(set_c)::value;
+        const int slot_now = gc % kWideRing;
+#pragma unroll
+        for (int k = 0; k < KSTEPS; ++k) {
+          if (k == KSTEPS - 1) {
+            // stage gc+1's tokens landed. Per K step the order is 2 DMA, then 2
+            // weight loads, so in steady state 30 operations were issued after
+            // the last DMA of that stage (its step's 2 weight loads, one stage
+            // of 16, three steps of 4); after the prologue (A0 B0 A1 B1 A2) only
+            // 28 follow A1 and A2. 28 is exact there and safe everywhere.
+            __builtin_amdgcn_sched_barrier(0);  // no memory operation crosses the count
+            wait_vmcnt<16 + 12>();
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): own LDS reads done
+            lds_barrier();
+            read_a(fa[(k + 1) & 1], (gc + 1) % kWideRing, 0);
+          } else {
+            read_a(fa[(k + 1) & 1], slot_now, k + 1);
+          }
+#pragma unroll
+          for (int i = 0; i < TM; ++i) {
+            if (i < TM / 2 || i < tma) {
+#pragma unroll
+              for (int j = 0; j < TN; ++j)
+                acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[SET][k][j], fa[k & 1][i],
+                                                                    acc[j][i], 0, 0, 0);
+            }
+          }
+          issue_a(2 * k);
+          issue_b(fb[SET][k], k);
+        }
+        advance_a();
+        advance_b();
+        ++gc;
+      };
+#pragma unroll 1
+      for (int kt = 0; kt < nk; kt += 2) {
+        stage(std::integral_constant<int, 0>{});
+        stage(std::integral_constant<int, 1>{});
+      }
+    }
+
+    // ---- epilogue through the LDS. A lane holds token row (lane & 31) of
+    // each 32-row block and 4 consecutive columns per 4-register group, so
+    // direct stores would touch 32 rows per instruction with 8 bytes each.
+    // Instead each wave stages one block of its output (64 columns = 128 B
+    // per row; SwiGLU: 32 columns = 64 B) in its own 4 KB of the ring slot
+    // just consumed, and reads it back so that CHUNKS consecutive lanes hold
+    // one row segment: every store instruction writes whole row segments.
+    // The slot is free until the next tile's DMA, which the barrier after
+    // the epilogue holds back. The staging swizzle (16-byte chunk XOR row
+    // bits, 8-byte half XOR row bit 4) keeps the 8-byte writes and the
+    // 16-byte reads free of bank conflicts.
+    {
+      constexpr int ROW_BYTES = SWIGLU ? 64 : 128;
+      constexpr int CHUNKS = ROW_BYTES / 16;
+      constexpr int ROWS_PER_INST = 64 / CHUNKS;
+      constexpr int JN = SWIGLU ? 1 : TN;
+      auto swz = [](int row) { return SWIGLU ? (row >> 2) & 3 : (row >> 1) & 7; };
+      char* stage_lds = reinterpret_cast<char*>(lds) + ((gc - 1) % kWideRing) * kWideStageBytes +
+                        wave * 4096;
+      const int r32 = lane & 31, h = lane >> 5;
+      const int col0 = SWIGLU ? ct.n0 + 32 * wave : ct.n0 + 64 * wave;  // this wave's columns
+      const int rl = lane / CHUNKS, cl = lane % CHUNKS;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        if (i >= tma) continue;
+#pragma unroll
+        for (int j = 0; j < JN; ++j) {
+#pragma unroll
+          for (int qg = 0; qg < 4; ++qg) {
+            float v[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              if constexpr (SWIGLU)
+                v[c] = silu_f(acc_read(acc[0][i][4 * qg + c])) * acc_read(acc[1][i][4 * qg + c]);
+              else
+                v[c] = acc_read(acc[j][i][4 * qg + c]);
+            }
+            u32x2_t o;
+            o[0] = pack_bf16x2(v[0], v[1]);
+            o[1] = pack_bf16x2(v[2], v[3]);
+            const int chunk = SWIGLU ? qg : 4 * j + qg;
+            const int off = r32 * ROW_BYTES + ((chunk ^ swz(r32)) * 16) + ((h ^ ((r32 >> 4) & 1)) * 8);
+            *reinterpret_cast<u32x2_t*>(stage_lds + off) = o;
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < 32 / ROWS_PER_INST; ++q) {
+          const int rr = q * ROWS_PER_INST + rl;
+          u32x4_t d = *reinterpret_cast<const u32x4_t*>(stage_lds + rr * ROW_BYTES +
+                                                        ((cl ^ swz(rr)) * 16));
+          if ((rr >> 4) & 1) d = u32x4_t{d[2], d[3], d[0], d[1]};  // halves were swapped
+          const int m = ct.m0 + 32 * i + rr;
+          const int col = col0 + 8 * cl;
+          if (m < ct.me && col < p.N)
+            *reinterpret_cast<u32x4_t*>(p.C + (int64_t)m * p.ldc + col) = d;
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's staging reads done
+      lds_barrier();                       // before the next DMA into the slot
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.f;
+    if (ct_idx + 1 < ntiles) ct = decode(ct_idx + 1);
+  }
+}
+
 // ------------------------------------------------------- small groups ----
 // Grouped GEMM for groups of at most 32*MT rows (decode-shaped layers: T <= 64
 // tokens, so every expert holds at most T rows). The work is streaming the
@@ -866,6 +1244,31 @@ static int launch_grouped_gemm(const GemmArgs& a, hipStream_t st) {
   return check_launch("grouped_gemm_kernel");
 }
 
+template <bool SWIGLU, bool GATHER>
+static int launch_wide_gemm(const GemmArgs& a, hipStream_t st) {
+  auto kern = wide_gemm_kernel<SWIGLU, GATHER>;
+  static std::once_flag once;
+  std::call_once(once, [&] {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kWideLdsBytes);
+  });
+  constexpr int OUT_N = SWIGLU ? 32 * kWideWaves : 64 * kWideWaves;
+  const int G = a.offsets != nullptr ? a.G : 1;
+  const int64_t nt = (a.N + OUT_N - 1) / OUT_N;
+  const int64_t upper = ((int64_t)(a.M + kWideBM - 1) / kWideBM + (a.offsets ? G : 0)) * nt;
+  int64_t nwg = std::min<int64_t>(upper, (int64_t)num_cus());
+  nwg = std::max<int64_t>(8, (nwg + 7) / 8 * 8);
+  if (GATHER) {
+    // every workgroup's tile count must fit the LDS row table
+    const int64_t chunks = (upper + kTileChunk - 1) / kTileChunk;
+    const int64_t xcd_max = (chunks + 7) / 8 * kTileChunk;
+    const int64_t per_xcd_min = (xcd_max + kWideRowTiles - 1) / kWideRowTiles;
+    nwg = std::max<int64_t>(nwg, 8 * per_xcd_min);
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)nwg), dim3(64 * kWideWaves), kWideLdsBytes, st, a);
+  return check_launch("wide_gemm_kernel");
+}
+
 template <int MT, bool SWIGLU, bool GATHER, bool TILED>
 static int launch_skinny_gemm(const GemmArgs& a, hipStream_t st) {
   const int G = a.offsets != nullptr ? a.G : 1;
@@ -906,6 +1309,10 @@ static int validate_gemm(const GemmArgs& a, const char* who) {
   if (a.b_tiled && (a.N % 32 || a.up_row_offset % 32))
     return fail(DSK_ERR_INVALID_ARG,
                 std::string(who) + ": tiled weights need N and the up-row offset in multiples of 32");
+  // the kernels address A rows by 32-bit byte offsets from A
+  const int64_t a_extent = (int64_t)(a.a_rows != nullptr ? a.a_rows_limit : a.M) * a.lda * 2;
+  if (a_extent > (int64_t)UINT32_MAX)
+    return fail(DSK_ERR_INVALID_ARG, std::string(who) + ": A operand larger than 4 GiB");
   return DSK_OK;
 }
 
@@ -916,6 +1323,13 @@ static int run_gemm_t(const GemmArgs& a, hipStream_t st) {
   // groups of at most 64 rows (decode): weight streaming kernel
   const int rows = a.max_group_rows > 0 ? std::min(a.max_group_rows, a.M) : a.M;
   if (rows <= kSkinnyMaxRows) return launch_skinny<SWIGLU, GATHER, TILED>(a, rows, st);
+#ifndef DSK_GEMM_WIDE
+#define DSK_GEMM_WIDE 1
+#endif
+  // fragment-tiled weights with K % 128 == 0 and 16-byte aligned output rows:
+  // one wave per SIMD, weights straight to registers
+  if (DSK_GEMM_WIDE && TILED && a.K % (2 * kWideBK) == 0 && aligned16(a.C) && a.ldc % 8 == 0)
+    return launch_wide_gemm<SWIGLU, GATHER>(a, st);
   constexpr int BM = DSK_GEMM_BM, BN = DSK_GEMM_BN, WM = DSK_GEMM_WAVES_M;
   constexpr int BK = DSK_GEMM_BK, ST = DSK_GEMM_STAGES;
   constexpr int WN = DSK_GEMM_WAVES_N;
