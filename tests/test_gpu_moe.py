@@ -352,6 +352,33 @@ def test_layer_forward_with_gate_matches_oracle(dsk, full_layer, tiled_layer, T,
     assert torch.equal(out, out2)
 
 
+@pytest.mark.parametrize("T", [16, 300])
+def test_layer_forward_graph_replay_matches_eager(dsk, full_layer, tiled_layer, T):
+    """The layer captured in a HIP graph (T=16: single routing launch and the
+    small-group GEMMs; T=300: scan and permutation kernels and the large-group
+    GEMMs) gives the eager result bit for bit on every replay, with eager layer
+    calls on other inputs between the replays."""
+    from ds_kernels import synthetic as syn
+    W, _, _, nsh, _ = full_layer
+    w1, w2 = tiled_layer
+    wgd = dsk.tile_weights(W.wg.to(torch.bfloat16)[None])[0].to(DEV)
+    bias = syn.zipf_router_bias().to(DEV)
+    x = syn.tokens(T).to(torch.bfloat16).to(DEV)
+    x_other = syn.tokens(T + 7).to(torch.bfloat16).to(DEV)
+    ref = dsk.moe_layer_forward(x, wgd, w1, w2, 6, nsh, gate_bias=bias)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = dsk.moe_layer_forward(x, wgd, w1, w2, 6, nsh, gate_bias=bias)
+    for _ in range(3):
+        out.zero_()
+        dsk.moe_layer_forward(x_other, wgd, w1, w2, 6, nsh, gate_bias=bias)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
+    del g
+
+
 def test_op_pipeline_matches_fused(dsk, full_layer):
     """Reference call sequence (routing->scan->dispatch->gemm1->swiglu->gemm2->combine),
     routed experts only, vs the oracle without shared experts."""
