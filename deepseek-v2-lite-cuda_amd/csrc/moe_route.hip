@@ -155,7 +155,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(
       }
       // rows of the always-on groups: group E+x row t is token t
       const int S = T * K;
-      for (int r = tid; r < n_extra_groups * T; r += kRouteThreads) token_map[S + r] = r % T;
+      for (int r = tid; r < n_extra_groups * T; r += blockDim.x) token_map[S + r] = r % T;
     }
   }
 }
@@ -320,28 +320,44 @@ __global__ __launch_bounds__(256) void combine_slots_kernel(
       }
     }
   }
+  constexpr int kPreExtra = 2;  // always-on group rows loaded with the slot rows
   for (int c = threadIdx.x; c < H / 8; c += blockDim.x) {
+    // every row load of this chunk is issued before the arithmetic, which
+    // then runs in the fixed order: slots ascending, then the extra groups
+    u32x4_t v[kMaxK], ve[kPreExtra];
+#pragma unroll
+    for (int k = 0; k < kMaxK; ++k)
+      if (s[k] != INT_MAX) v[k] = reinterpret_cast<const u32x4_t*>(y + (int64_t)s[k] * ldy)[c];
+#pragma unroll
+    for (int g = 0; g < kPreExtra; ++g)
+      if (g < n_extra_groups)
+        ve[g] = reinterpret_cast<const u32x4_t*>(
+            y + ((int64_t)extra_base + (int64_t)g * T + t) * ldy)[c];
     float acc[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[j] = 0.f;
 #pragma unroll
     for (int k = 0; k < kMaxK; ++k) {
       if (s[k] != INT_MAX) {
-        const u32x4_t v = reinterpret_cast<const u32x4_t*>(y + (int64_t)s[k] * ldy)[c];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          acc[2 * j] = fmaf(wt[k], bf16lo(v[j]), acc[2 * j]);
-          acc[2 * j + 1] = fmaf(wt[k], bf16hi(v[j]), acc[2 * j + 1]);
+          acc[2 * j] = fmaf(wt[k], bf16lo(v[k][j]), acc[2 * j]);
+          acc[2 * j + 1] = fmaf(wt[k], bf16hi(v[k][j]), acc[2 * j + 1]);
         }
       }
     }
     for (int g = 0; g < n_extra_groups; ++g) {
-      const int64_t row = (int64_t)extra_base + (int64_t)g * T + t;
-      const u32x4_t v = reinterpret_cast<const u32x4_t*>(y + row * ldy)[c];
+      u32x4_t vg;
+      if (g < kPreExtra) {
+        vg = g == 0 ? ve[0] : ve[1];
+      } else {
+        vg = reinterpret_cast<const u32x4_t*>(
+            y + ((int64_t)extra_base + (int64_t)g * T + t) * ldy)[c];
+      }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        acc[2 * j] += bf16lo(v[j]);
-        acc[2 * j + 1] += bf16hi(v[j]);
+        acc[2 * j] += bf16lo(vg[j]);
+        acc[2 * j + 1] += bf16hi(vg[j]);
       }
     }
     u32x4_t o;
@@ -480,7 +496,11 @@ int launch_route(const float* logits, int64_t ld, int n_parts, int64_t part_stri
                  float* w, int32_t* blk_hist, int32_t* local_rank, int32_t* counts,
                  int32_t* offsets, int32_t* token_map, int32_t* slot_of,
                  int n_extra_groups, hipStream_t st) {
-  hipLaunchKernelGGL(route_kernel, dim3(nchunks(T)), dim3(kRouteThreads), 0, st, logits,
+  // a single chunk (T <= 64) launches only the waves its tokens need (at
+  // least one: wave 0 does the chunk's scan; 64 lanes cover the 64 experts)
+  const int threads =
+      nchunks(T) == 1 ? kWave * std::max(1, (T + kTokPerWave - 1) / kTokPerWave) : kRouteThreads;
+  hipLaunchKernelGGL(route_kernel, dim3(nchunks(T)), dim3(threads), 0, st, logits,
                      ld, n_parts, part_stride, bias, T, E, K, idx, w, blk_hist, local_rank,
                      counts, offsets, token_map, slot_of, n_extra_groups);
   return check_launch("route_kernel");
