@@ -211,7 +211,9 @@ def bench_mla(dsk, syn, torch, ev, reps=20, warmup=5):
     rows = b * s
     t_norm = timed(lambda: dsk.rms_norm(kva[..., :512], W.kva_norm))
     t_rope = timed(lambda: dsk.rope(q[..., 128:], k_pe, cb, sb))
-    t_kvb = timed(lambda: dsk.kv_upproj(latent, W.kvb))
+    t_kvb = timed(lambda: dsk.kv_upproj(latent, W.kvb))      # tiled weight (the block's)
+    kvb_rm = dsk.untile_weights(W.kvb[None])[0].contiguous()
+    t_kvb_rm = timed(lambda: dsk.kv_upproj(latent, kvb_rm))  # reference layout
     t_block = timed(lambda: dm.mla_projections(x, W, cos, sin))
     norm_bytes = 2 * rows * 512 * 2 + 512 * 4
     rope_bytes = 2 * (rows * 16 * 64 * 2) + 2 * (rows * 64 * 2) + 2 * (s * 64 * 2)
@@ -232,7 +234,8 @@ def bench_mla(dsk, syn, torch, ev, reps=20, warmup=5):
             "kv_upproj": {"us": t_kvb * 1e3, "flops": kvb_flops,
                           "TFLOP/s": kvb_flops / (t_kvb * 1e-3) / 1e12,
                           "frac_of_bf16_peak": kvb_flops / (t_kvb * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
-                          "GB/s": gbs(kvb_bytes, t_kvb)},
+                          "GB/s": gbs(kvb_bytes, t_kvb), "weight_layout": "fragment-tiled",
+                          "us_row_major_weight": t_kvb_rm * 1e3},
         }}
     del q, kva, latent, k_pe
     # config 4: the decoder layer at 4 x 2048

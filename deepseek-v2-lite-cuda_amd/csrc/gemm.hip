@@ -1448,6 +1448,28 @@ extern "C" int dsk_linear(const dsk_bf16* x, int64_t ld_x, const dsk_bf16* w, ds
   return run_gemm(a, false, as_stream(stream));
 }
 
+extern "C" int dsk_linear_ex(const dsk_bf16* x, int64_t ld_x, const dsk_bf16* w,
+                             int weight_layout, dsk_bf16* out, int64_t ld_out, int M, int K,
+                             int N, void* stream) {
+  DSK_REQUIRE(weight_layout == DSK_LAYOUT_ROW_MAJOR || weight_layout == DSK_LAYOUT_TILED,
+              DSK_ERR_INVALID_ARG, "linear: weight_layout must be row-major or tiled");
+  if (weight_layout == DSK_LAYOUT_ROW_MAJOR)
+    return dsk_linear(x, ld_x, w, out, ld_out, M, K, N, stream);
+  DSK_REQUIRE(M >= 0, DSK_ERR_INVALID_ARG, "linear: M < 0");
+  if (M == 0) return DSK_OK;
+  GemmArgs a{};
+  a.A = x; a.lda = ld_x;
+  a.B = w; a.ldb = K; a.b_group_stride = 0;
+  a.C = out; a.ldc = ld_out;
+  a.offsets = nullptr; a.G = 1;
+  a.M = M; a.N = N; a.K = K;
+  a.b_tiled = 1;
+  int rc = validate_gemm(a, "linear");
+  if (rc) return rc;
+  DSK_REQUIRE(ld_out >= N, DSK_ERR_INVALID_ARG, "linear: ld_out < N");
+  return run_gemm(a, false, as_stream(stream));
+}
+
 extern "C" int dsk_kv_upproj(const dsk_bf16* normed_kv, int64_t ld_in, const dsk_bf16* weight,
                              dsk_bf16* out, int rows, int kv_lora_rank, int out_dim,
                              void* stream) {

@@ -2,12 +2,13 @@
 package's kernels (reference: src/reference/mla.py:251-393 DeepSeekMLA,
 src/reference/decoder_layer.py:108-139 DeepSeekDecoderLayer).
 
-Kernels used: `linear` (MFMA GEMM) for q_proj, kv_a_proj_with_mqa and o_proj,
-`rms_norm` straight on the 512-wide latent slice of the 576-wide kv_a output
-(row-strided, no copy), `kv_upproj`, `rope` on strided q_pe / k_pe views with
-the position tables broadcast over the batch (no materialised copies), and the
-fused MoE layer (`moe_layer_forward`). The causal attention core stays torch,
-as the survey scopes it, computed in fp32 with contiguous operands.
+Kernels used: `linear` (MFMA GEMM, weights prepacked in the fragment-tiled
+layout) for q_proj, kv_a_proj_with_mqa and o_proj, `rms_norm` straight on the
+512-wide latent slice of the 576-wide kv_a output (row-strided, no copy),
+`kv_upproj`, `rope` on strided q_pe / k_pe views with the position tables
+broadcast over the batch (no materialised copies), and the fused MoE layer
+(`moe_layer_forward`). The causal attention core stays torch, as the survey
+scopes it, at the reference's precision (bf16 products, fp32 softmax).
 """
 from __future__ import annotations
 
@@ -63,7 +64,8 @@ def yarn_cos_sin(seq_len: int, dim: int = 64, base: float = 10000.0, factor: flo
 # ----------------------------------------------------------------- weights --
 @dataclass
 class MLAWeights:
-    """bf16 projection weights ([out, in], nn.Linear order) and the fp32 latent norm."""
+    """bf16 projection weights ([out, in], nn.Linear order, or that matrix in the
+    fragment-tiled layout [out/32, in/16, 64, 8]) and the fp32 latent norm."""
     q: torch.Tensor          # [heads*(nope+rope), H]
     kva: torch.Tensor        # [kv_lora+rope, H]
     kva_norm: torch.Tensor   # [kv_lora] fp32
@@ -77,8 +79,12 @@ class MLAWeights:
     factor: float = 40.0     # YaRN scaling factor of DeepSeek-V2-Lite
 
     @staticmethod
-    def from_tensors(w: dict, device: torch.device) -> "MLAWeights":
-        bf = lambda t: t.to(device=device, dtype=torch.bfloat16).contiguous()  # noqa: E731
+    def from_tensors(w: dict, device: torch.device, tiled: bool = True) -> "MLAWeights":
+        """tiled: prepack the four projections once into the fragment-tiled
+        layout, which the projection GEMMs stream straight into registers."""
+        def bf(t):
+            t = t.to(device=device, dtype=torch.bfloat16).contiguous()
+            return tile_weights(t[None])[0] if tiled else t
         return MLAWeights(q=bf(w["q"]), kva=bf(w["kva"]),
                           kva_norm=w["kva_norm"].to(device=device, dtype=torch.float32),
                           kvb=bf(w["kvb"]), o=bf(w["o"]))

@@ -280,27 +280,39 @@ def moe_gemm2(swiglu_out: torch.Tensor, w2: torch.Tensor,
 
 def linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """x[..., K] @ weight[N, K]^T with the MFMA GEMM (bf16 in/out, fp32 acc).
-    x may be a row-strided view (last dim contiguous, row stride % 8 == 0)."""
+    x may be a row-strided view (last dim contiguous, row stride % 8 == 0).
+    weight is [N, K] row-major, or fragment-tiled [N/32, K/16, 64, 8]
+    (tile_weights(w[None])[0]), which runs the weight-streaming kernel."""
     op = "linear"
     _req(x.is_cuda and weight.is_cuda, f"{op}: tensors must be CUDA tensors.")
     _req(x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16, f"{op}: bfloat16 only.")
-    _req(weight.dim() == 2 and weight.is_contiguous(), f"{op}: weight must be contiguous 2-D.")
+    _req(weight.is_contiguous(), f"{op}: weight must be contiguous.")
     K = x.shape[-1]
-    N = weight.shape[0]
-    _req(weight.shape[1] == K, f"{op}: weight inner dim {weight.shape[1]} != {K}.")
+    tiled = weight.dim() == 4
+    if tiled:
+        _req(tuple(weight.shape[2:]) == (64, 8) and weight.shape[1] * 16 == K,
+             f"{op}: tiled weight must be [N/32, {K // 16}, 64, 8].")
+        N = weight.shape[0] * 32
+    else:
+        _req(weight.dim() == 2, f"{op}: weight must be 2-D [N, K] or tiled 4-D.")
+        N = weight.shape[0]
+        _req(weight.shape[1] == K, f"{op}: weight inner dim {weight.shape[1]} != {K}.")
     x2 = x.reshape(-1, K) if not x.is_contiguous() or x.dim() != 2 else x
     _req(x2.stride(-1) == 1, f"{op}: last dim of x must be contiguous.")
     M = x2.shape[0]
     out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
     if M:
         with torch.cuda.device(x.device):
-            check(lib.dsk_linear(x2.data_ptr(), x2.stride(0), weight.data_ptr(), out.data_ptr(),
-                                 N, M, K, N, stream_handle(x.device)), op)
+            check(lib.dsk_linear_ex(x2.data_ptr(), x2.stride(0), weight.data_ptr(),
+                                    1 if tiled else 0, out.data_ptr(), N, M, K, N,
+                                    stream_handle(x.device)), op)
     return out.view(*x.shape[:-1], N)
 
 
 def kv_upproj(normed_kv: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
-    """kv_b_proj up-projection (kv_upproj.cu:133-178): [..., 512] -> [..., out_dim]."""
+    """kv_b_proj up-projection (kv_upproj.cu:133-178): [..., 512] -> [..., out_dim].
+    weight is [out_dim, kv_lora_rank] as in the reference, or its fragment-tiled
+    form [out_dim/32, kv_lora_rank/16, 64, 8] (tile_weights(w[None])[0])."""
     op = "kv_upproj"
     _req(normed_kv.is_cuda and normed_kv.is_contiguous(),
          f"{op}: normed_kv must be a contiguous CUDA tensor.")
@@ -308,17 +320,29 @@ def kv_upproj(normed_kv: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     _req(normed_kv.dim() >= 2, f"{op}: normed_kv must have at least 2 dimensions.")
     _req(weight.is_cuda and weight.is_contiguous(), f"{op}: weight must be a contiguous CUDA tensor.")
     _req(weight.dtype == torch.bfloat16, f"{op}: weight must be bfloat16.")
-    _req(weight.dim() == 2, f"{op}: weight must be 2-D [out_dim, kv_lora_rank].")
     r = normed_kv.shape[-1]
-    _req(weight.shape[1] == r,
-         f"{op}: weight inner dim {weight.shape[1]} must match normed_kv last dim {r}.")
-    n = weight.shape[0]
+    tiled = weight.dim() == 4
+    if tiled:
+        _req(tuple(weight.shape[2:]) == (64, 8) and weight.shape[1] * 16 == r,
+             f"{op}: tiled weight must be [out_dim/32, {r // 16}, 64, 8].")
+        n = weight.shape[0] * 32
+    else:
+        _req(weight.dim() == 2, f"{op}: weight must be 2-D [out_dim, kv_lora_rank].")
+        _req(weight.shape[1] == r,
+             f"{op}: weight inner dim {weight.shape[1]} must match normed_kv last dim {r}.")
+        n = weight.shape[0]
     rows = normed_kv.numel() // r
     out = torch.empty((*normed_kv.shape[:-1], n), dtype=torch.bfloat16, device=normed_kv.device)
     if rows:
         with torch.cuda.device(normed_kv.device):
-            check(lib.dsk_kv_upproj(normed_kv.data_ptr(), r, weight.data_ptr(), out.data_ptr(),
-                                    rows, r, n, stream_handle(normed_kv.device)), op)
+            if tiled:
+                check(lib.dsk_linear_ex(normed_kv.data_ptr(), r, weight.data_ptr(), 1,
+                                        out.data_ptr(), n, rows, r, n,
+                                        stream_handle(normed_kv.device)), op)
+            else:
+                check(lib.dsk_kv_upproj(normed_kv.data_ptr(), r, weight.data_ptr(),
+                                        out.data_ptr(), rows, r, n,
+                                        stream_handle(normed_kv.device)), op)
     return out
 
 

@@ -167,6 +167,16 @@ int dsk_linear(const dsk_bf16* x, int64_t ld_x, const dsk_bf16* w,
 int dsk_kv_upproj(const dsk_bf16* normed_kv, int64_t ld_in,
                   const dsk_bf16* weight, dsk_bf16* out, int rows,
                   int kv_lora_rank, int out_dim, void* stream);
+/* dsk_linear with the weight in either layout: DSK_LAYOUT_ROW_MAJOR is
+ * dsk_linear; DSK_LAYOUT_TILED takes the weight [N, K] in the fragment-tiled
+ * order of the fused layer's expert weights (N % 32 == 0), which the one-wave-
+ * per-SIMD GEMM streams straight into registers when K % 128 == 0 and the
+ * output rows are 16-byte aligned. Serves the same projections as dsk_linear
+ * (mla.py:252-261 q_proj / kv_a_proj_with_mqa / kv_b_proj / o_proj, and the
+ * kv_upproj op's GEMM) with a prepacked weight. */
+int dsk_linear_ex(const dsk_bf16* x, int64_t ld_x, const dsk_bf16* w,
+                  int weight_layout, dsk_bf16* out, int64_t ld_out, int M,
+                  int K, int N, void* stream);
 
 /* --------------------------------------------------------------- rms_norm --
  * y = w * x * rsqrt(mean(x^2) + eps), fp32 math, one rounding of the output.

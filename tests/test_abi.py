@@ -75,6 +75,19 @@ def test_gemm_validation(dsk):
     assert rc == 1
 
 
+def test_linear_ex_validation(dsk):
+    lib = dsk.lib
+    # unknown weight layout
+    rc = lib.dsk_linear_ex(16, 2048, 16, 7, 16, 576, 4, 2048, 576, None)
+    assert rc == 1 and "layout" in _err(dsk)
+    # tiled weights need N % 32 == 0
+    rc = lib.dsk_linear_ex(16, 2048, 16, 1, 16, 100, 4, 2048, 100, None)
+    assert rc == 1 and "32" in _err(dsk)
+    # K must be a multiple of 64
+    rc = lib.dsk_linear_ex(16, 96, 16, 1, 16, 64, 4, 96, 64, None)
+    assert rc == 1 and "multiple of 64" in _err(dsk)
+
+
 def test_norm_rope_validation(dsk):
     lib = dsk.lib
     rc = lib.dsk_rms_norm(16, 511, 16, 16, 511, 4, 511, 1e-6, None)

@@ -104,6 +104,35 @@ def test_linear(dsk, M, K, N):
     assert max_rel_err(np32(out), ref) <= BF16_TOL
 
 
+@pytest.mark.parametrize("M,K,N", [(8, 2048, 3072), (130, 2048, 576), (1000, 512, 4096),
+                                   (300, 2048, 2048), (77, 128, 96), (50, 192, 64)])
+def test_linear_tiled_weight(dsk, M, K, N):
+    """The fragment-tiled weight path (one wave per SIMD, weights straight to
+    registers when K % 128 == 0; the 8-wave kernel otherwise) against fp32."""
+    g = torch.Generator().manual_seed(3 * M + N)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    wt = dsk.tile_weights(w[None])[0].to(DEV)
+    out = dsk.linear(x.to(DEV), wt)
+    ref = np32(x) @ np32(w).T
+    assert out.shape == (M, N)
+    assert max_rel_err(np32(out), ref) <= BF16_TOL
+    # same rounding as the row-major path: both accumulate in fp32 and round once
+    out_rm = dsk.linear(x.to(DEV), w.to(DEV))
+    assert max_rel_err(np32(out), np32(out_rm)) <= BF16_TOL
+
+
+@pytest.mark.parametrize("rows", [1, 64, 4096])
+def test_kv_upproj_tiled_weight(dsk, rows):
+    g = torch.Generator().manual_seed(rows + 7)
+    n = (torch.randn(rows, 512, generator=g) * 0.1).to(torch.bfloat16)
+    w = (torch.randn(4096, 512, generator=g) * 0.02).to(torch.bfloat16)
+    out = dsk.kv_upproj(n.to(DEV), dsk.tile_weights(w[None])[0].to(DEV))
+    ref = om.grouped_linear(np32(n), np32(w)[None], np.array([0, rows], np.int32))
+    assert out.shape == (rows, 4096)
+    assert max_rel_err(np32(out), ref) <= BF16_TOL
+
+
 # ------------------------------------------- configs 3 and 4 (composition) --
 def _bf(t):
     return t.to(torch.bfloat16).float().numpy()
