@@ -253,6 +253,64 @@ static int check_rope(const void* x, int64_t sb, int64_t sh, int64_t ss, const v
   return DSK_OK;
 }
 
+
+// ------------------------------------------------------- attention softmax --
+// In place over bf16 attention scores, rows of kv_len keys: the reference's
+// eager sequence (mla.py:366-381) in one pass, p = softmax over keys of
+// bf16(score * scale) + mask, in fp32, rounded once to bf16. The scaled score
+// is rounded to bf16 first because the reference multiplies the bf16 matmul
+// output by the scale in the model dtype. With causal masking, key j of query
+// i (query positions are the last q_len of the kv_len keys) is masked for
+// j > i + kv_len - q_len: its probability is 0 and its score is never read.
+// One wave per row; a lane holds 8 consecutive keys of each 512-key chunk in
+// registers (kv_len <= 512 * NC).
+template <int NC>
+__global__ __launch_bounds__(256) void attn_softmax_kernel(uint16_t* __restrict__ sc, int64_t ld,
+                                                           int64_t rows, int kv_len, int q_len,
+                                                           float scale, int causal) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;  // uniform over the wave
+  uint16_t* p = sc + row * ld;
+  const int qi = (int)(row % q_len);
+  const int limit = causal ? min(kv_len, qi + 1 + (kv_len - q_len)) : kv_len;
+  float v[NC][8];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int col = c * 512 + lane * 8;
+    u32x4_t w = u32x4_t{0u, 0u, 0u, 0u};
+    if (col < limit) w = *reinterpret_cast<const u32x4_t*>(p + col);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x = (e & 1) ? bf16hi(w[e / 2]) : bf16lo(w[e / 2]);
+      const float xs = bf16_to_f32(f32_to_bf16(x * scale));
+      v[c][e] = col + e < limit ? xs : -INFINITY;
+      mx = fmaxf(mx, v[c][e]);
+    }
+  }
+  mx = wave_max(mx);
+  float sum = 0.f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      v[c][e] = v[c][e] == -INFINITY ? 0.f : __expf(v[c][e] - mx);
+      sum += v[c][e];
+    }
+  sum = wave_sum(sum);
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int col = c * 512 + lane * 8;
+    if (col < kv_len) {
+      u32x4_t o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = pack_bf16x2(v[c][2 * e] / sum, v[c][2 * e + 1] / sum);
+      *reinterpret_cast<u32x4_t*>(p + col) = o;
+    }
+  }
+}
+
 }  // namespace dsk
 
 using namespace dsk;
@@ -318,4 +376,34 @@ extern "C" int dsk_rope(const dsk_bf16* x, int64_t sb, int64_t sh, int64_t ss,
                         dsk_bf16* out, int B, int Hh, int S, int d, void* stream) {
   return dsk_rope_qk(x, sb, sh, ss, nullptr, 0, 0, 0, cos_t, sin_t, cb, cs, out, nullptr, B, Hh,
                      0, S, d, stream);
+}
+
+extern "C" int dsk_attn_softmax(dsk_bf16* scores, int64_t ld, int64_t rows, int kv_len,
+                                int q_len, float scale, int causal, void* stream) {
+  DSK_REQUIRE(rows >= 0 && kv_len > 0 && q_len > 0, DSK_ERR_INVALID_ARG,
+              "attn_softmax: rows >= 0, kv_len > 0 and q_len > 0 required");
+  DSK_REQUIRE(kv_len % 8 == 0 && kv_len <= 4096, DSK_ERR_INVALID_ARG,
+              "attn_softmax: kv_len must be a multiple of 8 and at most 4096");
+  DSK_REQUIRE(rows % q_len == 0 && (!causal || q_len <= kv_len), DSK_ERR_INVALID_ARG,
+              "attn_softmax: rows must be a multiple of q_len, and q_len <= kv_len when causal");
+  if (rows == 0) return DSK_OK;
+  DSK_REQUIRE(scores != nullptr, DSK_ERR_NULL_PTR, "attn_softmax: NULL pointer");
+  DSK_REQUIRE(aligned16(scores) && ld % 8 == 0 && ld >= kv_len, DSK_ERR_ALIGNMENT,
+              "attn_softmax: rows must be 16-byte aligned with ld >= kv_len");
+  const unsigned grid = (unsigned)((rows + 3) / 4);
+  uint16_t* s = reinterpret_cast<uint16_t*>(scores);
+  hipStream_t st = as_stream(stream);
+  if (kv_len <= 512)
+    hipLaunchKernelGGL(attn_softmax_kernel<1>, dim3(grid), dim3(256), 0, st, s, ld, rows, kv_len,
+                       q_len, scale, causal);
+  else if (kv_len <= 1024)
+    hipLaunchKernelGGL(attn_softmax_kernel<2>, dim3(grid), dim3(256), 0, st, s, ld, rows, kv_len,
+                       q_len, scale, causal);
+  else if (kv_len <= 2048)
+    hipLaunchKernelGGL(attn_softmax_kernel<4>, dim3(grid), dim3(256), 0, st, s, ld, rows, kv_len,
+                       q_len, scale, causal);
+  else
+    hipLaunchKernelGGL(attn_softmax_kernel<8>, dim3(grid), dim3(256), 0, st, s, ld, rows, kv_len,
+                       q_len, scale, causal);
+  return check_launch("attn_softmax_kernel");
 }

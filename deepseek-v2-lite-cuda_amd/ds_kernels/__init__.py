@@ -5,6 +5,7 @@ HIP); importing this package without the built library raises ImportError.
 """
 from ._lib import LIB_PATH, DskError, lib  # noqa: F401  (loads libdsk.so or raises)
 from .ops import (  # noqa: F401
+    attn_softmax_,
     kv_upproj,
     linear,
     moe_combine,
@@ -36,7 +37,7 @@ from .moe_fused import (  # noqa: F401
 
 __all__ = [
     "moe_gate", "moe_routing", "moe_scan", "moe_dispatch", "moe_combine", "swiglu", "moe_gemm1",
-    "moe_gemm1_swiglu", "moe_gemm2", "rms_norm", "kv_upproj", "linear", "rope",
+    "moe_gemm1_swiglu", "moe_gemm2", "rms_norm", "kv_upproj", "linear", "rope", "attn_softmax_",
     "prepack_experts", "prepack_with_shared", "pack_tensors", "tile_weights", "untile_weights",
     "FusedMoELayer",
     "fused_moe_forward", "moe_fused_forward_logits", "moe_layer_forward",

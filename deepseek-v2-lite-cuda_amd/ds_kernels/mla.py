@@ -7,8 +7,10 @@ layout) for q_proj, kv_a_proj_with_mqa and o_proj, `rms_norm` straight on the
 512-wide latent slice of the 576-wide kv_a output (row-strided, no copy),
 `kv_upproj`, `rope` on strided q_pe / k_pe views with the position tables
 broadcast over the batch (no materialised copies), and the fused MoE layer
-(`moe_layer_forward`). The causal attention core stays torch, as the survey
-scopes it, at the reference's precision (bf16 products, fp32 softmax).
+(`moe_layer_forward`). In the causal attention core the two batched products
+stay torch, as the survey scopes it; the scale, causal mask, fp32 softmax and
+bf16 rounding between them are one pass of `attn_softmax_`, at the reference's
+precision.
 """
 from __future__ import annotations
 
@@ -121,18 +123,17 @@ def mla_forward(x: torch.Tensor, W: MLAWeights, cos: torch.Tensor, sin: torch.Te
                 eps: float = 1e-6) -> torch.Tensor:
     """DeepSeekMLA.forward (mla.py:295-393) for positions 0..s-1 with the causal
     mask: projections on this package's kernels, o_proj on the MFMA GEMM, and
-    the attention core in torch at the reference's precision (mla.py:366-384):
-    bf16 Q.K^T, scale, causal mask, softmax in fp32 rounded to bf16, bf16 .V.
-    The right-hand operands are made contiguous before the batched products.
+    the attention core at the reference's precision (mla.py:366-384): bf16 Q.K^T
+    and .V in torch (right-hand operands made contiguous before the batched
+    products), the scale, causal mask, fp32 softmax and bf16 rounding in one
+    pass of attn_softmax_.
     x: bf16 [b, s, H] -> bf16 [b, s, H]."""
     b, s, H = x.shape
     q_nope, q_rot, k_nope, v, k_rot, _ = mla_projections(x, W, cos, sin, eps)
     q = torch.cat([q_nope, q_rot], dim=-1)                             # [b,h,s,192]
     k = torch.cat([k_nope, k_rot.expand(b, W.n_heads, s, W.rope_dim)], dim=-1)
-    scores = torch.matmul(q, k.transpose(-1, -2).contiguous()) * W.softmax_scale
-    causal = torch.ones(s, s, dtype=torch.bool, device=x.device).triu(1)
-    scores.masked_fill_(causal, float("-inf"))
-    p = torch.softmax(scores, dim=-1, dtype=torch.float32).to(torch.bfloat16)
+    scores = torch.matmul(q, k.transpose(-1, -2).contiguous())        # bf16 [b,h,s,s]
+    p = ops.attn_softmax_(scores, W.softmax_scale, causal=True)       # scale, mask, softmax
     o = torch.matmul(p, v.contiguous())                                # [b,h,s,v]
     o = o.transpose(1, 2).reshape(b, s, W.n_heads * W.v_dim)
     return ops.linear(o, W.o)

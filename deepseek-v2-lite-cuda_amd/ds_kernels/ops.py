@@ -389,6 +389,27 @@ def _rope_strides(t: torch.Tensor, name: str):
     return sb, (sh if h > 1 else 0), ss
 
 
+def attn_softmax_(scores: torch.Tensor, scale: float, causal: bool = True) -> torch.Tensor:
+    """In place over bf16 scores [..., q_len, kv_len] (last dim contiguous, rows
+    16-byte aligned): softmax_fp32(bf16(scores * scale) + causal mask) rounded to
+    bf16, the eager sequence of DeepSeekMLA.forward (mla.py:366-381) in one pass.
+    Query i sees keys j <= i + kv_len - q_len when causal. Returns scores."""
+    op = "attn_softmax"
+    _req(scores.is_cuda, f"{op}: scores must be a CUDA tensor.")
+    _dtype(scores, torch.bfloat16, "scores", op)
+    _req(scores.dim() >= 2 and scores.stride(-1) == 1, f"{op}: last dim must be contiguous.")
+    q_len, kv_len = scores.shape[-2], scores.shape[-1]
+    flat = scores.view(-1, kv_len) if scores.is_contiguous() else None
+    _req(flat is not None, f"{op}: scores must be contiguous.")
+    rows = flat.shape[0]
+    if rows:
+        with torch.cuda.device(scores.device):
+            check(lib.dsk_attn_softmax(flat.data_ptr(), kv_len, rows, kv_len, q_len,
+                                       float(scale), 1 if causal else 0,
+                                       stream_handle(scores.device)), op)
+    return scores
+
+
 def rope(q_pe: torch.Tensor, k_pe: torch.Tensor, cos: torch.Tensor,
          sin: torch.Tensor) -> List[torch.Tensor]:
     """Interleaved -> half RoPE on q_pe [b,h,s,d] and k_pe [b,1,s,d] with the

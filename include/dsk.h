@@ -212,6 +212,18 @@ int dsk_rope_qk(const dsk_bf16* q, int64_t qsb, int64_t qsh, int64_t qss,
                 int64_t cs, dsk_bf16* q_out, dsk_bf16* k_out, int B, int Hq,
                 int Hk, int S, int d, void* stream);
 
+/* ------------------------------------------------------ attention softmax --
+ * In place over bf16 attention scores [rows, kv_len] (row stride ld): the
+ * eager sequence of DeepSeekMLA.forward (mla.py:366-381) in one pass,
+ *   p = bf16(softmax_fp32(bf16(score * scale) + causal_mask)),
+ * with key j of query i masked when causal and j > i + kv_len - q_len (the row's
+ * query index is row % q_len). Masked probabilities are written as 0 and their
+ * scores are not read. The reference has no kernel for this: it replaces four
+ * torch passes over the scores (scale, mask, fp32 softmax, cast) of the
+ * decoder layer's attention core. kv_len % 8 == 0, kv_len <= 4096. */
+int dsk_attn_softmax(dsk_bf16* scores, int64_t ld, int64_t rows, int kv_len,
+                     int q_len, float scale, int causal, void* stream);
+
 /* ------------------------------------------------------- fused MoE layer --
  * The whole DeepSeekMoE forward (moe.py:77-109) on the device:
  *   route -> stable permutation -> grouped GEMM1+SwiGLU -> grouped GEMM2 ->

@@ -88,6 +88,18 @@ def test_linear_ex_validation(dsk):
     assert rc == 1 and "multiple of 64" in _err(dsk)
 
 
+def test_attn_softmax_validation(dsk):
+    lib = dsk.lib
+    rc = lib.dsk_attn_softmax(16, 100, 64, 100, 8, 0.1, 1, None)
+    assert rc == 1 and "multiple of 8" in _err(dsk)
+    rc = lib.dsk_attn_softmax(16, 8192, 64, 8192, 8, 0.1, 1, None)
+    assert rc == 1 and "4096" in _err(dsk)
+    rc = lib.dsk_attn_softmax(16, 64, 60, 64, 8, 0.1, 1, None)
+    assert rc == 1 and "q_len" in _err(dsk)
+    rc = lib.dsk_attn_softmax(16, 64, 64, 64, 128, 0.1, 1, None)
+    assert rc == 1 and "q_len" in _err(dsk)
+
+
 def test_norm_rope_validation(dsk):
     lib = dsk.lib
     rc = lib.dsk_rms_norm(16, 511, 16, 16, 511, 4, 511, 1e-6, None)

@@ -133,6 +133,40 @@ def test_kv_upproj_tiled_weight(dsk, rows):
     assert max_rel_err(np32(out), ref) <= BF16_TOL
 
 
+def _softmax_ref(sc: torch.Tensor, scale: float, causal: bool) -> torch.Tensor:
+    """CPU fp32 restatement of mla.py:366-381 on the same bf16 scores: scores *
+    scale rounded to bf16, causal mask (query i of the last q_len positions sees
+    keys j <= i + kv_len - q_len), softmax in fp32 (torch), rounded to bf16."""
+    q_len, kv_len = sc.shape[-2:]
+    x = (sc.float() * scale).to(torch.bfloat16).float()
+    if causal:
+        i = torch.arange(q_len)[:, None]
+        j = torch.arange(kv_len)[None, :]
+        x = x.masked_fill(j > i + (kv_len - q_len), float("-inf"))
+    return torch.softmax(x, dim=-1).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("shape,causal", [((2, 3, 64, 64), True), ((1, 2, 40, 520), True),
+                                          ((2, 16, 128, 2048), True), ((1, 1, 8, 4096), True),
+                                          ((3, 5, 16, 1024), False), ((4, 7, 72), False)])
+def test_attn_softmax_matches_torch(dsk, shape, causal):
+    g = torch.Generator().manual_seed(sum(shape))
+    sc = (torch.randn(*shape, generator=g) * 6).to(torch.bfloat16)
+    scale = 0.1147
+    ref = _softmax_ref(sc, scale, causal)
+    out = dsk.attn_softmax_(sc.to(DEV), scale, causal=causal).cpu()
+    # bf16 outputs of the same fp32 softmax: at most one bf16 ulp apart
+    diff = (out.float() - ref.float()).abs()
+    assert float(diff.max()) <= 2 ** -7 * float(ref.float().abs().max())
+    assert max_rel_err(np32(out), np32(ref)) <= BF16_TOL
+    if causal:  # masked keys are exactly zero, every row sums to one
+        q_len, kv_len = shape[-2:]
+        i = torch.arange(q_len)[:, None]
+        j = torch.arange(kv_len)[None, :]
+        assert bool((out.float()[..., j > i + (kv_len - q_len)] == 0).all())
+    np.testing.assert_allclose(out.float().sum(-1).numpy(), 1.0, atol=2e-2)
+
+
 # ------------------------------------------- configs 3 and 4 (composition) --
 def _bf(t):
     return t.to(torch.bfloat16).float().numpy()
