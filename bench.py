@@ -246,7 +246,53 @@ def bench_mla(dsk, syn, torch, ev, reps=20, warmup=5):
     out["config4_decoder_layer"] = {
         "shape": "b=4, s=2048, causal; MLA (16 heads) + MoE (64 routed top-6 + 2 shared)",
         "layer_ms": t_layer, "tokens_per_s": b4 * s / (t_layer * 1e-3)}
+    del P, x4
+    out["latent_cache_decode"] = bench_latent_decode(dsk, torch, dm, W, timed, dev, g)
     return out
+
+
+def bench_latent_decode(dsk, torch, dm, W, timed, dev, g):
+    """Decode over the latent KV cache: the attention op alone (reads every
+    cached 1152-byte row once; HBM-bound) at a few (batch, cache length)
+    points, and one whole decode step (projections, cache append, absorbed
+    attention, W_UV, o_proj) for one new token after 4095 cached ones, beside
+    the full-sequence recompute at 4096 that a cache-less forward pays."""
+    A = dsk.AbsorbedMLAWeights.from_mla(W)
+    cos, sin = dm.yarn_cos_sin(8192, device=dev)
+    cos, sin = cos.to(torch.bfloat16), sin.to(torch.bfloat16)
+    gbs = lambda nbytes, ms: nbytes / (ms * 1e-3) / 1e9  # noqa: E731
+    res = {"attention_op": []}
+    for b, L, n in ((1, 4096, 1), (4, 4096, 1), (16, 4096, 1), (1, 4096, 8)):
+        rows = torch.randn(b, L, 576, generator=g).to(torch.bfloat16).to(dev)
+        q_abs = (torch.randn(b * n, 16, 512, generator=g) * 0.05).to(torch.bfloat16).to(dev)
+        q_pe = torch.randn(b * n, 16, 64, generator=g).to(torch.bfloat16).to(dev)
+        o = torch.empty(b * n, 16, 512, dtype=torch.bfloat16, device=dev)
+        t = timed(lambda: dsk.mla_decode_attention(q_abs, q_pe, rows[..., :512], rows[..., 512:],
+                                                   cos, sin, W.softmax_scale, out=o))
+        nbytes = b * L * 576 * 2 + 2 * b * n * 16 * (512 + 64 + 512) + 2 * L * 64 * 2
+        res["attention_op"].append({"batch": b, "cache_len": L, "new_tokens": n, "us": t * 1e3,
+                                    "algorithmic_bytes": nbytes, "GB/s": gbs(nbytes, t),
+                                    "frac_of_8TB/s": gbs(nbytes, t) / PEAK_HBM_GBS})
+        del rows, q_abs, q_pe, o
+    L = 4096
+    x = torch.randn(1, L, 2048, generator=g).to(torch.bfloat16).to(dev)
+    cache = dsk.LatentKVCache.for_inference(1, max_seq=L, device=dev)
+    dsk.mla_decode_forward(x[:, :L - 1], W, cache, cos, sin, A)   # prefix into the cache
+    x1 = x[:, L - 1:].contiguous()
+
+    def step():
+        cache._len = L - 1          # re-append position L-1 each call
+        dsk.mla_decode_forward(x1, W, cache, cos, sin, A)
+
+    t_step = timed(step)
+    cf, sf = dm.yarn_cos_sin(L, device=dev)
+    t_full = timed(lambda: dm.mla_forward(x, W, cf, sf), per_graph=1)
+    res["decode_step"] = {"batch": 1, "cache_len": L, "us": t_step * 1e3,
+                          "full_sequence_recompute_us": t_full * 1e3,
+                          "note": "one new token: q / kv_a projections, cache append, absorbed "
+                                  "attention, W_UV, o_proj; versus mla_forward over all 4096 "
+                                  "positions (what a forward without a cache recomputes)"}
+    return res
 
 
 def cpu_baseline(W, syn, budget_s):

@@ -1,0 +1,165 @@
+"""Latent KV cache and absorbed-MLA decode on it.
+
+LatentKVCache mirrors src/kernels/mla_cache.py:29-219 (same constructor,
+properties, update/get/reset, errors and repr): per token it keeps the raw
+compressed latent (kv_lora_rank, before the RMSNorm) and the raw shared RoPE
+key (rope_head_dim, before RoPE), 576 bf16 values instead of the 5120 of the
+up-projected K and V. Both live in one [bsz, max_seq, 576] buffer, the layout
+kv_a_proj_with_mqa produces, so one cache row is one contiguous 1152-byte read
+for the attention kernel; `kv_latent` and `k_pe_cache` are views of it with the
+reference's shapes.
+
+mla_decode_forward runs DeepSeekMLA.forward (src/reference/mla.py:295-393) for
+new tokens against the cache in the absorbed form: the kv_b up-projection is
+folded into the query (q_abs = (W_UK * w)^T q_nope per head) and into the
+output ((W_UV * w) o_lat per head), and `ops.mla_decode_attention` attends
+straight over the cached raw latents, computing each key's RMS scale and RoPE
+on the fly. The reference itself has no attention over its cache (mla.py:7
+recomputes K and V for the whole sequence).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional, Tuple
+
+import torch
+
+from . import ops
+from .expert_prepack import untile_weights
+from .mla import MLAWeights
+
+
+class LatentKVCache:
+    """Pre-allocated compressed KV cache for MLA (mla_cache.py:29-96).
+
+    kv_latent  [bsz, max_seq, kv_lora_rank]   raw latent (pre-norm), a view
+    k_pe_cache [bsz, max_seq, rope_head_dim]  raw shared RoPE key, a view
+    """
+
+    def __init__(self, bsz: int, max_seq: int, kv_lora_rank: int = 512, rope_head_dim: int = 64,
+                 device="cuda", dtype: torch.dtype = torch.bfloat16):
+        if not isinstance(bsz, int) or bsz < 1:
+            raise ValueError(f"bsz must be a positive integer, got {bsz}")
+        if not isinstance(max_seq, int) or max_seq < 1:
+            raise ValueError(f"max_seq must be a positive integer, got {max_seq}")
+        self.bsz = bsz
+        self.max_seq = max_seq
+        self.kv_lora_rank = kv_lora_rank
+        self.rope_head_dim = rope_head_dim
+        self.device = torch.device(device)
+        self.dtype = dtype
+        self._len = 0
+        self.rows = torch.zeros((bsz, max_seq, kv_lora_rank + rope_head_dim), dtype=dtype,
+                                device=self.device)
+        self.kv_latent = self.rows[..., :kv_lora_rank]
+        self.k_pe_cache = self.rows[..., kv_lora_rank:]
+
+    @property
+    def current_len(self) -> int:
+        """Number of tokens currently stored."""
+        return self._len
+
+    @property
+    def remaining_capacity(self) -> int:
+        """Number of tokens that can still be appended."""
+        return self.max_seq - self._len
+
+    @property
+    def memory_bytes(self) -> int:
+        """Bytes held by the latent and RoPE-key planes (mla_cache.py:92-98)."""
+        return (self.kv_latent.numel() + self.k_pe_cache.numel()) * self.rows.element_size()
+
+    def update(self, compressed_kv: torch.Tensor, k_pe: torch.Tensor) -> None:
+        """Append new tokens (mla_cache.py:102-143): compressed_kv [bsz, n,
+        kv_lora_rank] and k_pe [bsz, n, rope_head_dim], converted to the cache's
+        device and dtype. ValueError for non-3-D inputs, RuntimeError when the
+        cache would exceed max_seq (nothing is written then)."""
+        if compressed_kv.dim() != 3:
+            raise ValueError("compressed_kv must be 3D [bsz, new_tokens, kv_lora_rank], "
+                             f"got shape {tuple(compressed_kv.shape)}")
+        if k_pe.dim() != 3:
+            raise ValueError("k_pe must be 3D [bsz, new_tokens, rope_head_dim], "
+                             f"got shape {tuple(k_pe.shape)}")
+        n = compressed_kv.shape[1]
+        if self._len + n > self.max_seq:
+            raise RuntimeError(f"KV cache overflow: current_len={self._len}, new_tokens={n}, "
+                               f"max_seq={self.max_seq}. Increase max_seq or reset the cache.")
+        slot = slice(self._len, self._len + n)
+        self.kv_latent[:, slot, :] = compressed_kv.to(self.device, self.dtype)
+        self.k_pe_cache[:, slot, :] = k_pe.to(self.device, self.dtype)
+        self._len += n
+
+    def get(self, seq_len: Optional[int] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Views of the first seq_len tokens (default: all stored), mla_cache.py:145-169.
+        ValueError if more tokens are asked for than are stored."""
+        if seq_len is None:
+            seq_len = self._len
+        if seq_len > self._len:
+            raise ValueError(f"Requested seq_len={seq_len} but cache only has {self._len} tokens.")
+        return self.kv_latent[:, :seq_len, :], self.k_pe_cache[:, :seq_len, :]
+
+    def reset(self) -> None:
+        """Start a new sequence; keeps the buffers (mla_cache.py:171-176)."""
+        self._len = 0
+
+    def __repr__(self) -> str:
+        used = (self._len * (self.kv_lora_rank + self.rope_head_dim) * self.rows.element_size()
+                * self.bsz) / (1024 ** 2)
+        total = self.memory_bytes / (1024 ** 2)
+        return (f"LatentKVCache(bsz={self.bsz}, tokens={self._len}/{self.max_seq}, "
+                f"used={used:.2f}MB/{total:.2f}MB, device={self.device}, dtype={self.dtype})")
+
+    @classmethod
+    def for_inference(cls, bsz: int, max_seq: int = 4096, device="cuda") -> "LatentKVCache":
+        """bf16 cache with DeepSeek-V2-Lite's widths (512 + 64), mla_cache.py:201-219."""
+        return cls(bsz=bsz, max_seq=max_seq, kv_lora_rank=512, rope_head_dim=64, device=device,
+                   dtype=torch.bfloat16)
+
+
+@dataclass
+class AbsorbedMLAWeights:
+    """kv_b folded for the absorbed form, with the latent RMSNorm weight w in it:
+    w_uk[h] = W_UK[h] * w (the k_nope rows of head h, [nope, kv_lora]) and
+    w_uv_t[h] = (W_UV[h] * w)^T ([kv_lora, v_dim]); both bf16, contiguous."""
+    w_uk: torch.Tensor
+    w_uv_t: torch.Tensor
+
+    @staticmethod
+    def from_mla(W: MLAWeights) -> "AbsorbedMLAWeights":
+        kvb = W.kvb if W.kvb.dim() == 2 else untile_weights(W.kvb[None])[0]
+        h, nope, vd = W.n_heads, W.nope, W.v_dim
+        kv = kvb.float().view(h, nope + vd, W.kv_lora) * W.kva_norm.float()[None, None, :]
+        return AbsorbedMLAWeights(
+            w_uk=kv[:, :nope].to(torch.bfloat16).contiguous(),
+            w_uv_t=kv[:, nope:].transpose(1, 2).to(torch.bfloat16).contiguous())
+
+
+def mla_decode_forward(x: torch.Tensor, W: MLAWeights, cache: LatentKVCache, cos: torch.Tensor,
+                       sin: torch.Tensor, absorbed: Optional[AbsorbedMLAWeights] = None,
+                       eps: float = 1e-6) -> torch.Tensor:
+    """DeepSeekMLA.forward (mla.py:295-393) for new tokens x: bf16 [bsz, n, H] at
+    positions cache.current_len .. + n - 1, causal over the cached prefix and
+    among themselves. Appends their raw latent and k_pe to the cache and
+    returns bf16 [bsz, n, H]. cos/sin: bf16 [positions, rope_dim] tables
+    indexed by position (yarn_cos_sin of at least the final length)."""
+    op = "mla_decode_forward"
+    ops._req(x.dim() == 3 and x.dtype == torch.bfloat16, f"{op}: x must be bf16 [bsz, n, H].")
+    b, n, H = x.shape
+    ops._req(b == cache.bsz, f"{op}: x has batch {b}, the cache {cache.bsz}.")
+    ops._req(cache.kv_lora_rank == W.kv_lora and cache.rope_head_dim == W.rope_dim,
+             f"{op}: cache widths do not match the weights.")
+    A = absorbed if absorbed is not None else AbsorbedMLAWeights.from_mla(W)
+    h, nope, r = W.n_heads, W.nope, W.rope_dim
+    q = ops.linear(x, W.q).view(b * n, h, nope + r)      # [T, h, 192]
+    kva = ops.linear(x, W.kva)                             # [b, n, 576]
+    cache.update(kva[..., :W.kv_lora], kva[..., W.kv_lora:])
+    L = cache.current_len
+    q_nope = q[..., :nope].transpose(0, 1).contiguous()    # [h, T, nope]
+    q_abs = torch.bmm(q_nope, A.w_uk)                      # [h, T, kv_lora]
+    latent, k_pe = cache.get(L)
+    o_lat = torch.empty((h, b * n, W.kv_lora), dtype=torch.bfloat16, device=x.device)
+    ops.mla_decode_attention(q_abs.transpose(0, 1), q[..., nope:], latent, k_pe, cos, sin,
+                             W.softmax_scale, eps, out=o_lat.transpose(0, 1))
+    o = torch.bmm(o_lat, A.w_uv_t)                         # [h, T, v_dim]
+    o = o.transpose(0, 1).reshape(b, n, h * W.v_dim)
+    return ops.linear(o, W.o)

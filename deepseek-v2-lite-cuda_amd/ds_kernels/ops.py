@@ -410,6 +410,56 @@ def attn_softmax_(scores: torch.Tensor, scale: float, causal: bool = True) -> to
     return scores
 
 
+def mla_decode_attention(q_abs: torch.Tensor, q_pe: torch.Tensor, latent: torch.Tensor,
+                         k_pe: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, scale: float,
+                         eps: float = 1e-6, out: torch.Tensor = None) -> torch.Tensor:
+    """Absorbed MLA attention of T = bsz * n new tokens over the raw latent
+    cache (the attention of mla.py:356-384 on cached tokens, latent RMSNorm
+    and RoPE applied on the fly).
+    q_abs: bf16 [T, 16, 512] ((W_UK * w)^T q_nope per head); q_pe: bf16
+    [T, 16, 64], raw (pre-RoPE); latent / k_pe: bf16 [bsz, L, 512] / [bsz, L, 64]
+    cache views sharing their batch and token strides, the last n tokens being
+    the new ones; cos/sin: bf16 [>= L, 64] by position. All may be strided
+    views with a contiguous last dim. Returns bf16 [T, 16, 512] (into `out` if
+    given): sum_j softmax_j r_j x_j per head."""
+    op = "mla_decode_attention"
+    for t, nm in ((q_abs, "q_abs"), (q_pe, "q_pe"), (latent, "latent"), (k_pe, "k_pe"),
+                  (cos, "cos"), (sin, "sin")):
+        _req(isinstance(t, torch.Tensor) and t.is_cuda, f"{op}: {nm} must be a CUDA tensor.")
+        _dtype(t, torch.bfloat16, nm, op)
+        _req(t.stride(-1) == 1, f"{op}: {nm} last dim must be contiguous.")
+    _req(q_abs.dim() == 3 and q_abs.shape[1:] == (16, 512), f"{op}: q_abs must be [T, 16, 512].")
+    T = q_abs.shape[0]
+    _req(q_pe.shape == (T, 16, 64), f"{op}: q_pe must be [T, 16, 64].")
+    _req(latent.dim() == 3 and latent.shape[2] == 512, f"{op}: latent must be [bsz, L, 512].")
+    b, L = latent.shape[0], latent.shape[1]
+    _req(k_pe.shape == (b, L, 64), f"{op}: k_pe must be [bsz, L, 64].")
+    _req(latent.stride()[:2] == k_pe.stride()[:2],
+         f"{op}: latent and k_pe must share batch and token strides.")
+    _req(b > 0 and T % b == 0, f"{op}: T={T} is not a multiple of bsz={b}.")
+    n = T // b
+    _req(n <= L, f"{op}: {n} new tokens but only {L} in the cache.")
+    _req(cos.shape == sin.shape and cos.dim() == 2 and cos.shape[1] == 64 and cos.shape[0] >= L,
+         f"{op}: cos/sin must be [>= {L}, 64].")
+    cos, sin = cos.contiguous(), sin.contiguous()
+    if out is None:
+        out = torch.empty((T, 16, 512), dtype=torch.bfloat16, device=q_abs.device)
+    _req(out.shape == (T, 16, 512) and out.dtype == torch.bfloat16 and out.stride(-1) == 1,
+         f"{op}: out must be bf16 [T, 16, 512] with a contiguous last dim.")
+    if T == 0:
+        return out
+    ws = _ws(lib.dsk_mla_decode_workspace_size(b, n, L), q_abs.device)
+    ld_batch = latent.stride(0) if b > 1 else L * latent.stride(1)
+    with torch.cuda.device(q_abs.device):
+        check(lib.dsk_mla_decode_attention(
+            q_abs.data_ptr(), q_abs.stride(0), q_abs.stride(1), q_pe.data_ptr(), q_pe.stride(0),
+            q_pe.stride(1), latent.data_ptr(), k_pe.data_ptr(), latent.stride(1), ld_batch,
+            cos.data_ptr(), sin.data_ptr(), float(eps), float(scale), b, n, L, out.data_ptr(),
+            out.stride(0), out.stride(1), ws.data_ptr(), ws.numel(),
+            stream_handle(q_abs.device)), op)
+    return out
+
+
 def rope(q_pe: torch.Tensor, k_pe: torch.Tensor, cos: torch.Tensor,
          sin: torch.Tensor) -> List[torch.Tensor]:
     """Interleaved -> half RoPE on q_pe [b,h,s,d] and k_pe [b,1,s,d] with the

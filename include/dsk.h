@@ -224,6 +224,36 @@ int dsk_rope_qk(const dsk_bf16* q, int64_t qsb, int64_t qsh, int64_t qss,
 int dsk_attn_softmax(dsk_bf16* scores, int64_t ld, int64_t rows, int kv_len,
                      int q_len, float scale, int causal, void* stream);
 
+/* ----------------------------------------------- latent-cache decode attention --
+ * Absorbed multi-head latent attention of new tokens over the latent KV cache
+ * of LatentKVCache (src/kernels/mla_cache.py:29-219), which holds per token the
+ * raw compressed latent x (pre-RMSNorm, 512) and the raw shared RoPE key
+ * (pre-RoPE, 64). Query token t = b * q_len + i sits at cache position
+ * kv_len - q_len + i; for each head h < 16 and key j <= that position:
+ *   s_j     = scale * (q_abs[t,h] . (r_j x_j) + rope(q_pe[t,h]) . rope(k_pe_j))
+ *   o[t,h]  = sum_j softmax(s)_j r_j x_j        (fp32, stored as bf16)
+ * with r_j = rsqrt(mean(x_j^2) + eps) and rope as in dsk_rope (angles of the
+ * row's position in cos/sin [positions, 64], which must cover kv_len rows).
+ * q_abs[t,h] (512) is (W_UK[h] * norm_weight)^T q_nope[t,h]; the caller
+ * applies (W_UV[h] * norm_weight) and o_proj to o. Element strides: q_abs at
+ * t * qa_tok + h * qa_head, q_pe (raw, pre-RoPE) at t * qp_tok + h * qp_head,
+ * cache token j of sequence b at b * ld_batch + j * ld_tok in latent and in
+ * k_pe (the two may interleave in one 576-wide row), o at t * o_tok +
+ * h * o_head. This is the attention of DeepSeekMLA.forward (mla.py:318-384)
+ * over the cached prefix plus the new tokens; the reference has no kernel for
+ * it (it recomputes K and V for the whole sequence). */
+size_t dsk_mla_decode_workspace_size(int batch, int q_len, int kv_len);
+int dsk_mla_decode_attention(const dsk_bf16* q_abs, int64_t qa_tok,
+                             int64_t qa_head, const dsk_bf16* q_pe,
+                             int64_t qp_tok, int64_t qp_head,
+                             const dsk_bf16* latent, const dsk_bf16* k_pe,
+                             int64_t ld_tok, int64_t ld_batch,
+                             const dsk_bf16* cos_tab, const dsk_bf16* sin_tab,
+                             float eps, float scale, int batch, int q_len,
+                             int kv_len, dsk_bf16* o_latent, int64_t o_tok,
+                             int64_t o_head, void* workspace, size_t bytes,
+                             void* stream);
+
 /* ------------------------------------------------------- fused MoE layer --
  * The whole DeepSeekMoE forward (moe.py:77-109) on the device:
  *   route -> stable permutation -> grouped GEMM1+SwiGLU -> grouped GEMM2 ->

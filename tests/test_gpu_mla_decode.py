@@ -1,0 +1,119 @@
+"""GPU parity of decode over the latent KV cache: mla_decode_forward (absorbed
+MLA attention on the raw cached latents, dsk_mla_decode_attention) against the
+oracle's full-sequence DeepSeekMLA.forward (oracle/mla.py mla_forward, fp32,
+causal), whose rows for the positions of the new tokens are what incremental
+decoding must reproduce. Prefix fills, single-token steps, multi-token steps,
+batches, chunk-boundary lengths and the empty-cache start are covered; the
+bar is the bf16 one (max relative error <= 2e-2)."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import BF16_TOL, max_rel_err, np32
+from oracle import mla as ol
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module")
+def setup():
+    import ds_kernels as dsk
+    from ds_kernels import mla as dm
+    from ds_kernels import synthetic as syn
+    w = syn.mla_weights()
+    W = dm.MLAWeights.from_tensors(w, torch.device(DEV))
+    A = dsk.AbsorbedMLAWeights.from_mla(W)
+    wn = {k: (np32(v.to(torch.bfloat16)) if k != "kva_norm" else v.numpy()) for k, v in w.items()}
+    cos, sin = dm.yarn_cos_sin(2048)
+    return dsk, W, A, wn, cos.to(torch.bfloat16).to(DEV), sin.to(torch.bfloat16).to(DEV)
+
+
+def _oracle(x, wn):
+    return ol.mla_forward(np32(x), wn["q"], wn["kva"], wn["kva_norm"], wn["kvb"], wn["o"])
+
+
+def _run_steps(setup, x, steps):
+    """Feed x [b, S, H] to a fresh cache in consecutive pieces of the given sizes."""
+    dsk, W, A, _, cos, sin = setup
+    b, S, _ = x.shape
+    cache = dsk.LatentKVCache(b, S + 3, device=DEV)
+    outs, pos = [], 0
+    for n in steps:
+        outs.append(dsk.mla_decode_forward(x[:, pos:pos + n].to(DEV), W, cache, cos, sin, A))
+        pos += n
+    assert pos == S and cache.current_len == S
+    torch.cuda.synchronize()
+    return torch.cat(outs, 1).cpu(), cache
+
+
+@pytest.mark.parametrize("b,steps", [
+    (1, [1, 1, 1, 1]),                 # starts from an empty cache
+    (1, [50, 1, 1, 1, 7, 1]),          # prefill, single steps, a multi-token step
+    (2, [127, 1, 1, 1]),               # crosses the 64-key chunk boundary at 128
+    (2, [63, 2, 64, 1]),
+    (1, [700, 1, 5]),                  # many chunks
+])
+def test_decode_matches_full_sequence_oracle(setup, b, steps):
+    S = sum(steps)
+    g = torch.Generator().manual_seed(7 * S + b)
+    x = torch.randn(b, S, 2048, generator=g).to(torch.bfloat16)
+    out, _ = _run_steps(setup, x, steps)
+    ref = _oracle(x, setup[3])
+    assert out.shape == (b, S, 2048)
+    err = max_rel_err(np32(out), ref)
+    assert err <= BF16_TOL, f"max rel err {err:.3e}"
+    # every step's rows on their own (a late step must not hide in the global max)
+    pos = 0
+    for n in steps:
+        e = max_rel_err(np32(out[:, pos:pos + n]), ref[:, pos:pos + n])
+        assert e <= BF16_TOL, f"rows {pos}..{pos + n}: {e:.3e}"
+        pos += n
+
+
+def test_cache_holds_raw_projection_rows(setup):
+    """The cache stores kv_a_proj_with_mqa's raw output (pre-norm latent,
+    pre-RoPE key), as mla_cache.py:33-35 documents."""
+    dsk, W, A, wn, cos, sin = setup
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(2, 9, 2048, generator=g).to(torch.bfloat16)
+    _, cache = _run_steps(setup, x, [4, 5])
+    lat, pe = cache.get()
+    kva = ol.linear(np32(x), wn["kva"])
+    assert max_rel_err(np32(lat), kva[..., :512]) <= BF16_TOL
+    assert max_rel_err(np32(pe), kva[..., 512:]) <= BF16_TOL
+
+
+def test_decode_attention_op_strided_inputs(setup):
+    """The op on a separately allocated, non-interleaved cache (latent and k_pe
+    in their own tensors with equal strides) and a strided output view gives the
+    same result as on the cache's interleaved rows."""
+    dsk, W, A, wn, cos, sin = setup
+    g = torch.Generator().manual_seed(9)
+    b, n, L = 2, 3, 150
+    rows = torch.randn(b, L, 576, generator=g).to(torch.bfloat16).to(DEV)
+    q_abs = (torch.randn(b * n, 16, 512, generator=g) * 0.1).to(torch.bfloat16).to(DEV)
+    q_pe = torch.randn(b * n, 16, 64, generator=g).to(torch.bfloat16).to(DEV)
+    scale = W.softmax_scale
+    a = dsk.mla_decode_attention(q_abs, q_pe, rows[..., :512], rows[..., 512:], cos, sin, scale)
+    lat = torch.zeros(b, L, 576, dtype=torch.bfloat16, device=DEV)
+    pe = torch.zeros(b, L, 576, dtype=torch.bfloat16, device=DEV)
+    lat[..., :512] = rows[..., :512]
+    pe[..., :64] = rows[..., 512:]
+    out = torch.zeros(16, b * n, 512, dtype=torch.bfloat16, device=DEV)
+    dsk.mla_decode_attention(q_abs, q_pe, lat[..., :512], pe[..., :64], cos, sin, scale,
+                             out=out.transpose(0, 1))
+    torch.cuda.synchronize()
+    assert torch.equal(out.transpose(0, 1).cpu(), a.cpu())
+
+
+def test_decode_op_rejects_bad_shapes(setup):
+    dsk, W, A, wn, cos, sin = setup
+    rows = torch.zeros(1, 8, 576, dtype=torch.bfloat16, device=DEV)
+    q_abs = torch.zeros(9, 16, 512, dtype=torch.bfloat16, device=DEV)
+    q_pe = torch.zeros(9, 16, 64, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match="new tokens"):
+        dsk.mla_decode_attention(q_abs, q_pe, rows[..., :512], rows[..., 512:], cos, sin, 0.1)
+    with pytest.raises(RuntimeError, match="cos/sin"):
+        dsk.mla_decode_attention(q_abs[:2], q_pe[:2], rows[..., :512], rows[..., 512:],
+                                 cos[:4], sin[:4], 0.1)

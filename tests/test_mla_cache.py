@@ -1,0 +1,85 @@
+"""LatentKVCache API (the buffer bookkeeping of src/kernels/mla_cache.py:29-219)
+on CPU tensors: shapes, views, append/read-back, overflow and argument errors,
+memory accounting and repr. The reference ships no tests for this class; the
+expected values follow from its documented contract (mla_cache.py:1-23: 576
+bf16 values per token, 4.5 MB per layer at bsz=1, max_seq=4096)."""
+import pytest
+import torch
+
+from ds_kernels import LatentKVCache
+
+
+def _tokens(b, n, seed, width):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(b, n, width, generator=g).to(torch.bfloat16)
+
+
+def test_shapes_and_memory_of_the_inference_cache():
+    c = LatentKVCache.for_inference(1, device="cpu")
+    assert c.kv_latent.shape == (1, 4096, 512) and c.k_pe_cache.shape == (1, 4096, 64)
+    assert c.kv_latent.dtype == torch.bfloat16
+    assert c.memory_bytes == 576 * 4096 * 2 == int(4.5 * 1024 ** 2)
+    assert c.current_len == 0 and c.remaining_capacity == 4096
+    assert repr(c) == ("LatentKVCache(bsz=1, tokens=0/4096, used=0.00MB/4.50MB, device=cpu, "
+                       "dtype=torch.bfloat16)")
+
+
+def test_update_get_round_trip_and_views():
+    c = LatentKVCache(2, 10, device="cpu")
+    lat1, pe1 = _tokens(2, 3, 0, 512), _tokens(2, 3, 1, 64)
+    lat2, pe2 = _tokens(2, 4, 2, 512), _tokens(2, 4, 3, 64)
+    c.update(lat1, pe1)
+    c.update(lat2, pe2)
+    assert c.current_len == 7 and c.remaining_capacity == 3
+    lat, pe = c.get()
+    assert torch.equal(lat, torch.cat([lat1, lat2], 1)) and torch.equal(pe, torch.cat([pe1, pe2], 1))
+    lat, pe = c.get(3)
+    assert torch.equal(lat, lat1) and torch.equal(pe, pe1)
+    # zero-copy views of the cache buffers
+    assert lat.data_ptr() == c.kv_latent.data_ptr() and pe.data_ptr() == c.k_pe_cache.data_ptr()
+    # one 576-wide row per token: latent then RoPE key, as kv_a_proj_with_mqa emits them
+    assert torch.equal(c.rows[:, :7, :512], c.get()[0])
+    assert torch.equal(c.rows[:, 3:7, 512:], pe2)
+    assert c.get(0)[0].shape == (2, 0, 512)
+
+
+def test_update_converts_dtype():
+    c = LatentKVCache(1, 4, device="cpu")
+    lat = torch.randn(1, 2, 512)
+    c.update(lat, torch.randn(1, 2, 64))
+    assert torch.equal(c.get()[0], lat.to(torch.bfloat16))
+
+
+def test_overflow_raises_and_writes_nothing():
+    c = LatentKVCache(1, 5, device="cpu")
+    c.update(_tokens(1, 4, 0, 512), _tokens(1, 4, 1, 64))
+    before = c.rows.clone()
+    with pytest.raises(RuntimeError, match="KV cache overflow: current_len=4, new_tokens=2, max_seq=5"):
+        c.update(_tokens(1, 2, 2, 512), _tokens(1, 2, 3, 64))
+    assert c.current_len == 4 and torch.equal(c.rows, before)
+    c.update(_tokens(1, 1, 4, 512), _tokens(1, 1, 5, 64))
+    assert c.current_len == 5 and c.remaining_capacity == 0
+
+
+def test_argument_errors():
+    with pytest.raises(ValueError, match="bsz"):
+        LatentKVCache(0, 4, device="cpu")
+    with pytest.raises(ValueError, match="max_seq"):
+        LatentKVCache(1, 2.5, device="cpu")
+    c = LatentKVCache(1, 4, device="cpu")
+    with pytest.raises(ValueError, match="compressed_kv must be 3D"):
+        c.update(torch.zeros(2, 512), torch.zeros(1, 2, 64))
+    with pytest.raises(ValueError, match="k_pe must be 3D"):
+        c.update(torch.zeros(1, 2, 512), torch.zeros(2, 64))
+    with pytest.raises(ValueError, match="seq_len=1"):
+        c.get(1)
+
+
+def test_reset_keeps_buffers_and_repr_counts_used_tokens():
+    c = LatentKVCache(2, 1024, device="cpu")
+    ptr = c.rows.data_ptr()
+    c.update(_tokens(2, 512, 0, 512), _tokens(2, 512, 1, 64))
+    # used = 512 tokens * 576 * 2 B * bsz 2 = 1.125 MiB of 2.25 MiB
+    assert "tokens=512/1024, used=1.12MB/2.25MB" in repr(c)
+    c.reset()
+    assert c.current_len == 0 and c.remaining_capacity == 1024 and c.rows.data_ptr() == ptr
