@@ -50,12 +50,8 @@ constexpr int kLatPad = kLat + 8;  // LDS row pitch: 16 B of padding spreads row
 // angles of one position: returns (rot[k], rot[k + 32]) per pair, where
 // rot[k] = x[2k] cos[k] - x[2k+1] sin[k] and
 // rot[k + 32] = x[2k+1] cos[k + 32] + x[2k] sin[k + 32] (mla.py:196-205).
-__device__ __forceinline__ u32x4_t rope_pairs(u32x4_t xv, const uint16_t* crow,
-                                              const uint16_t* srow, int k0) {
-  const u32x2_t clo = *reinterpret_cast<const u32x2_t*>(crow + k0);
-  const u32x2_t chi = *reinterpret_cast<const u32x2_t*>(crow + kRope / 2 + k0);
-  const u32x2_t slo = *reinterpret_cast<const u32x2_t*>(srow + k0);
-  const u32x2_t shi = *reinterpret_cast<const u32x2_t*>(srow + kRope / 2 + k0);
+__device__ __forceinline__ u32x4_t rope_pairs(u32x4_t xv, u32x2_t clo, u32x2_t chi, u32x2_t slo,
+                                              u32x2_t shi) {
   u32x4_t rv;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -68,6 +64,23 @@ __device__ __forceinline__ u32x4_t rope_pairs(u32x4_t xv, const uint16_t* crow,
     rv[e] = pack_bf16x2(x0 * c_lo - x1 * s_lo, x1 * c_hi + x0 * s_hi);
   }
   return rv;
+}
+
+// The angles of pairs k0..k0+3 of one position: cos[k0..], cos[k0+32..], sin[k0..], sin[k0+32..].
+struct RopeAngles {
+  u32x2_t clo, chi, slo, shi;
+};
+__device__ __forceinline__ RopeAngles load_angles(const uint16_t* crow, const uint16_t* srow,
+                                                  int k0) {
+  RopeAngles r;
+  r.clo = *reinterpret_cast<const u32x2_t*>(crow + k0);
+  r.chi = *reinterpret_cast<const u32x2_t*>(crow + kRope / 2 + k0);
+  r.slo = *reinterpret_cast<const u32x2_t*>(srow + k0);
+  r.shi = *reinterpret_cast<const u32x2_t*>(srow + kRope / 2 + k0);
+  return r;
+}
+__device__ __forceinline__ u32x4_t rope_pairs(u32x4_t xv, const RopeAngles& r) {
+  return rope_pairs(xv, r.clo, r.chi, r.slo, r.shi);
 }
 
 struct DecodeArgs {
@@ -121,32 +134,10 @@ __global__ __launch_bounds__(256, 2) void attn_split_kernel(DecodeArgs a) {
 
   const uint16_t* xbase = a.latent + (int64_t)b * a.ld_batch;
   const uint16_t* pbase = a.kpe + (int64_t)b * a.ld_batch;
-  // query fragments (operand B of the scores, head r16): loop invariant
-  u32x4_t qv[kLat / 32], qr[kRope / 32];
-  {
-    const uint16_t* qa = a.q_abs + tok * a.qa_tok + r16 * a.qa_head;
-    const uint16_t* qp = a.q_pe + tok * a.qp_tok + r16 * a.qp_head;
-#pragma unroll
-    for (int ks = 0; ks < kLat / 32; ++ks)
-      qv[ks] = *reinterpret_cast<const u32x4_t*>(qa + ks * 32 + 8 * g);
-#pragma unroll
-    for (int ks = 0; ks < kRope / 32; ++ks) {
-      const int d0 = ks * 32 + 8 * g;
-      qr[ks] = rope_pairs(*reinterpret_cast<const u32x4_t*>(qp + d0),
-                          a.cos_t + (int64_t)pos_q * kRope, a.sin_t + (int64_t)pos_q * kRope,
-                          d0 / 2);
-    }
-  }
-
-  float m_run = -INFINITY;  // running max of head r16 (same in every wave)
-  float l_lane = 0.f;       // this lane's share of the running sum of head r16
-  floatx4_t acc[8];
-#pragma unroll
-  for (int t = 0; t < 8; ++t) acc[t] = floatx4_t{0.f, 0.f, 0.f, 0.f};
-
-  // cache fragments of the block being loaded: lane holds key r16 of the wave's
-  // 16, dims 8g..8g+7 of each 32-dim step
+  // cache fragments of a block: lane holds key r16 of the wave's 16, dims
+  // 8g..8g+7 of each 32-dim step, and that key's RoPE angles
   u32x4_t xv[kLat / 32], pv[kRope / 32];
+  RopeAngles ka[kRope / 32];
   auto load_block = [&](int kb) {
     const int key = kb + wave * 16 + r16;
     const int keyc = key < L ? key : L - 1;  // clamped for loads; masked below
@@ -156,15 +147,57 @@ __global__ __launch_bounds__(256, 2) void attn_split_kernel(DecodeArgs a) {
     for (int ks = 0; ks < kLat / 32; ++ks)
       xv[ks] = *reinterpret_cast<const u32x4_t*>(xrow + ks * 32 + 8 * g);
 #pragma unroll
-    for (int ks = 0; ks < kRope / 32; ++ks)
+    for (int ks = 0; ks < kRope / 32; ++ks) {
       pv[ks] = *reinterpret_cast<const u32x4_t*>(prow + ks * 32 + 8 * g);
+      ka[ks] = load_angles(a.cos_t + (int64_t)keyc * kRope, a.sin_t + (int64_t)keyc * kRope,
+                           (ks * 32 + 8 * g) / 2);
+    }
   };
+  // query fragments (operand B of the scores, head r16): loop invariant. The
+  // 16 KB of q_abs rows are fetched once per workgroup and handed to the waves
+  // through LDS rows 0..15 of s_x (free until the first block is staged); the
+  // first block's loads are issued in between, so both latencies overlap.
+  u32x4_t qv[kLat / 32], qr[kRope / 32];
+  {
+    u32x4_t qst[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = threadIdx.x + 256 * j;  // 16 heads x 64 pieces of 16 B
+      qst[j] = *reinterpret_cast<const u32x4_t*>(a.q_abs + tok * a.qa_tok +
+                                                 (c >> 6) * a.qa_head + (c & 63) * 8);
+    }
+    const uint16_t* qp = a.q_pe + tok * a.qp_tok + r16 * a.qp_head;
+    u32x4_t qpv[kRope / 32];
+#pragma unroll
+    for (int ks = 0; ks < kRope / 32; ++ks)
+      qpv[ks] = *reinterpret_cast<const u32x4_t*>(qp + ks * 32 + 8 * g);
+    if (k_begin < k_end) load_block(k_begin);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = threadIdx.x + 256 * j;
+      *reinterpret_cast<u32x4_t*>(&s_x[c >> 6][(c & 63) * 8]) = qst[j];
+    }
+#pragma unroll
+    for (int ks = 0; ks < kRope / 32; ++ks) {
+      const int d0 = ks * 32 + 8 * g;
+      qr[ks] = rope_pairs(qpv[ks], load_angles(a.cos_t + (int64_t)pos_q * kRope,
+                                               a.sin_t + (int64_t)pos_q * kRope, d0 / 2));
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < kLat / 32; ++ks)
+      qv[ks] = *reinterpret_cast<const u32x4_t*>(&s_x[r16][ks * 32 + 8 * g]);
+    __syncthreads();  // every wave holds its copy before s_x is overwritten
+  }
+
+  float m_run = -INFINITY;  // running max of head r16 (same in every wave)
+  float l_lane = 0.f;       // this lane's share of the running sum of head r16
+  floatx4_t acc[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) acc[t] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+
   for (int kb = k_begin; kb < k_end; kb += kBlock) {
-    load_block(kb);  // (two workgroups per CU overlap one's loads with the other's math)
-    if (kb != k_begin) __syncthreads();  // previous block's P.X reads of s_x / s_p done
     // ---- scores of the wave's 16 keys: latent part, RMS statistics, RoPE part
-    const int key = kb + wave * 16 + r16;
-    const int keyc = key < L ? key : L - 1;
     floatx4_t acc_n = {0.f, 0.f, 0.f, 0.f}, acc_r = {0.f, 0.f, 0.f, 0.f};
     float ss = 0.f;
 #pragma unroll
@@ -182,8 +215,7 @@ __global__ __launch_bounds__(256, 2) void attn_split_kernel(DecodeArgs a) {
     }
 #pragma unroll
     for (int ks = 0; ks < kRope / 32; ++ks) {
-      const u32x4_t kv = rope_pairs(pv[ks], a.cos_t + (int64_t)keyc * kRope,
-                                    a.sin_t + (int64_t)keyc * kRope, (ks * 32 + 8 * g) / 2);
+      const u32x4_t kv = rope_pairs(pv[ks], ka[ks]);
       acc_r = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kv),
                                                       __builtin_bit_cast(bf16x8_t, qr[ks]),
                                                       acc_r, 0, 0, 0);
@@ -248,6 +280,10 @@ __global__ __launch_bounds__(256, 2) void attn_split_kernel(DecodeArgs a) {
                                                          acc[t], 0, 0, 0);
       }
     }
+    if (kb + kBlock < k_end) {
+      load_block(kb + kBlock);  // in flight while the waves meet at the barrier
+      __syncthreads();          // this block's P.X reads of s_x / s_p done
+    }
   }
 
   // ---- split statistics and partial output
@@ -271,13 +307,15 @@ __global__ __launch_bounds__(256, 2) void attn_split_kernel(DecodeArgs a) {
 }
 
 // Merge of a query token's splits: out = sum_s exp(m_s - m) O_s / sum_s exp(m_s - m) l_s
-// per head. Workgroup (slice, token): 256 threads, each owning 4 consecutive
-// fragment-order floats (one head, 4 dims) of the 8192; the splits are summed
-// in a fixed order, 8 loads in flight. Splits with no visible key (m_s = -inf)
-// contribute nothing and their partials are not read.
+// per head. Workgroup (slice, token) owns 16 fragment-order float4s (256 B of
+// each split's partial, one per head); its 16 split lanes sum consecutive
+// sixteenths of the splits, 4 loads in flight, and the sixteenths are added in
+// a fixed order (no atomics). Splits with no visible key (m_s = -inf)
+// contribute nothing.
 __global__ __launch_bounds__(256) void attn_merge_kernel(DecodeArgs a) {
-  __shared__ float s_f[kMaxSplits][kHeads];  // exp(m_s - m) / den per split and head
+  __shared__ float s_f[kMaxSplits][kHeads];  // exp(m_s - m) per split and head
   __shared__ float s_red[16][kHeads];
+  __shared__ floatx4_t s_acc[16][16];
   const int S = a.n_splits;
   const int64_t tok = blockIdx.y;
   const float* ml = a.part_ml + tok * S * 2 * kHeads;
@@ -304,31 +342,39 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(DecodeArgs a) {
   for (int i = 0; i < 16; ++i) den += s_red[i][h16];  // fixed order
   const float inv = 1.f / den;  // split 0 holds key 0, so den >= 1
 
-  // fragment-order element e4 = blockIdx.x * 256 + threadIdx.x (a float4)
-  const int e4 = blockIdx.x * 256 + threadIdx.x;
-  const int wv = e4 >> 9, t = (e4 >> 6) & 7, ln = e4 & 63;
-  const int head = ln & 15;  // == h16: this thread's inv is its head's
+  const int e4 = blockIdx.x * 16 + h16;  // fragment-order float4 index
+  const int ln = e4 & 63;
+  const int head = ln & 15;              // == h16
   const float* po = a.part_o + tok * S * (kHeads * kLat) + (int64_t)e4 * 4;
+  const int s0 = (S * sl) >> 4, s1 = (S * (sl + 1)) >> 4;
   floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
-  int s = 0;
-  for (; s + 8 <= S; s += 8) {
-    floatx4_t v[8];
+  int s = s0;
+  for (; s + 4 <= s1; s += 4) {
+    floatx4_t v[4];
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < 4; ++u)
       v[u] = *reinterpret_cast<const floatx4_t*>(po + (int64_t)(s + u) * (kHeads * kLat));
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < 4; ++u) {
       const float f = s_f[s + u][head];
       if (f != 0.f) acc += f * v[u];
     }
   }
-  for (; s < S; ++s) {
+  for (; s < s1; ++s) {
     const float f = s_f[s][head];
     if (f != 0.f) acc += f * *reinterpret_cast<const floatx4_t*>(po + (int64_t)s * (kHeads * kLat));
   }
-  uint16_t* o = a.out + tok * a.o_tok + head * a.o_head;
+  s_acc[sl][h16] = acc;
+  __syncthreads();
+  if (sl == 0) {
+    acc = s_acc[0][h16];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) o[frag_dim(wv, t, ln, i)] = f32_to_bf16(acc[i] * inv);
+    for (int i = 1; i < 16; ++i) acc += s_acc[i][h16];  // fixed order
+    const int wv = e4 >> 9, t = (e4 >> 6) & 7;
+    uint16_t* o = a.out + tok * a.o_tok + head * a.o_head;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[frag_dim(wv, t, ln, i)] = f32_to_bf16(acc[i] * inv);
+  }
 }
 
 }  // namespace dsk
@@ -337,12 +383,16 @@ using namespace dsk;
 
 namespace {
 
+#ifndef DSK_DECODE_WGS
+#define DSK_DECODE_WGS 512
+#endif
+
 // Key splits per query token: enough workgroups to cover the chip about twice
-// (512), at most kMaxSplits, at least one 64-key block each.
+// (DSK_DECODE_WGS), at most kMaxSplits, at least one 64-key block each.
 void split_plan(int batch, int q_len, int kv_len, int* n_splits, int* split_blocks) {
   const int blocks = (kv_len + kBlock - 1) / kBlock;
   const int64_t tokens = (int64_t)batch * q_len;
-  int want = (int)std::min<int64_t>(blocks, std::max<int64_t>(1, (512 + tokens - 1) / tokens));
+  int want = (int)std::min<int64_t>(blocks, std::max<int64_t>(1, (DSK_DECODE_WGS + tokens - 1) / tokens));
   want = std::min(want, kMaxSplits);
   int per = (blocks + want - 1) / want;
   *split_blocks = per;
@@ -422,7 +472,7 @@ extern "C" int dsk_mla_decode_attention(const dsk_bf16* q_abs, int64_t qa_tok, i
   hipLaunchKernelGGL(attn_split_kernel, dim3(S, q_len, batch), dim3(256), 0, st, a);
   int rc = check_launch("attn_split_kernel");
   if (rc) return rc;
-  hipLaunchKernelGGL(attn_merge_kernel, dim3(kHeads * kLat / 4 / 256, batch * q_len), dim3(256),
+  hipLaunchKernelGGL(attn_merge_kernel, dim3(kHeads * kLat / 4 / 16, batch * q_len), dim3(256),
                      0, st, a);
   return check_launch("attn_merge_kernel");
 }
