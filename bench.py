@@ -21,7 +21,8 @@ Also reported on the same line:
   cpu_baseline  the CPU oracle (numpy restatement of DeepSeekMoE.forward) timed
                 on a bounded sample (config 0, T=64 fp32) on this host's cores.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--profile | --decode-only T | --mla-only]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+                       [--profile | --decode-only T | --mla-only | --mla-decode-only]
 """
 from __future__ import annotations
 
@@ -165,6 +166,35 @@ def bench_decode(dsk, syn, torch, F, W, packed, T, steps, ev, copies):
             "algorithmic_bytes": bytes_, "GB/s": gbs, "frac_of_8TB/s": gbs / PEAK_HBM_GBS}
 
 
+def graph_timer(torch, ev, reps=20, warmup=5):
+    """Returns timed(fn, per_graph=10): the median time of fn on the GPU, with
+    per_graph back-to-back calls captured in a HIP graph (so host-side Python cost
+    between launches does not leave the GPU idle), replayed `reps` times between
+    HIP events on the stream."""
+    def timed(fn, per_graph=10):
+        st = torch.cuda.current_stream().cuda_stream
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(per_graph):
+                fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        evs = ev.create(2 * reps)
+        for i in range(reps):
+            ev.rt.hipEventRecord(evs[2 * i], st)
+            graph.replay()
+            ev.rt.hipEventRecord(evs[2 * i + 1], st)
+        torch.cuda.synchronize()
+        t = sorted(ev.ms(evs[2 * i], evs[2 * i + 1]) / per_graph for i in range(reps))
+        ev.destroy(evs)
+        del graph
+        return t[len(t) // 2]
+    return timed
+
+
 def bench_mla(dsk, syn, torch, ev, reps=20, warmup=5):
     """BASELINE configs 3 and 4: the MLA projection block at 8 x 2048 (rms_norm and
     rope against HBM, kv_upproj against MFMA, each timed with HIP events on the
@@ -182,32 +212,7 @@ def bench_mla(dsk, syn, torch, ev, reps=20, warmup=5):
     kva = dsk.linear(x, W.kva)
     latent = dsk.rms_norm(kva[..., :512], W.kva_norm)
     k_pe = kva[..., 512:].view(b, s, 1, 64).transpose(1, 2)
-    st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
-
-    def timed(fn, per_graph=10):
-        """Median time of fn on the GPU: per_graph back-to-back calls captured in
-        a HIP graph (so host-side Python cost between launches does not leave
-        the GPU idle), replayed `reps` times between HIP events on the stream."""
-        for _ in range(warmup):
-            fn()
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            for _ in range(per_graph):
-                fn()
-        graph.replay()
-        torch.cuda.synchronize()
-        evs = ev.create(2 * reps)
-        for i in range(reps):
-            ev.rt.hipEventRecord(evs[2 * i], st())
-            graph.replay()
-            ev.rt.hipEventRecord(evs[2 * i + 1], st())
-        torch.cuda.synchronize()
-        t = sorted(ev.ms(evs[2 * i], evs[2 * i + 1]) / per_graph for i in range(reps))
-        ev.destroy(evs)
-        del graph
-        return t[len(t) // 2]
-
+    timed = graph_timer(torch, ev, reps, warmup)
     rows = b * s
     t_norm = timed(lambda: dsk.rms_norm(kva[..., :512], W.kva_norm))
     t_rope = timed(lambda: dsk.rope(q[..., 128:], k_pe, cb, sb))
@@ -392,6 +397,8 @@ def main():
                     help="run only the 1 GiB device copy used to scale the HBM counters")
     ap.add_argument("--mla-only", action="store_true",
                     help="only the MLA projection block and decoder layer (for profiling)")
+    ap.add_argument("--mla-decode-only", action="store_true",
+                    help="only the latent-cache decode attention and decode step (for profiling)")
     args = ap.parse_args()
     if args.calibrate_copy:
         calibrate_copy(3)
@@ -411,6 +418,13 @@ def main():
     torch.cuda.set_device(dev)
     if args.mla_only:
         print(json.dumps(bench_mla(dsk, syn, torch, HipEvents())), flush=True)
+        return
+    if args.mla_decode_only:
+        from ds_kernels import mla as dm
+        W = dm.MLAWeights.from_tensors(syn.mla_weights(), dev)
+        timed = graph_timer(torch, HipEvents())
+        print(json.dumps(bench_latent_decode(dsk, torch, dm, W, timed, dev,
+                                             torch.Generator().manual_seed(1234))), flush=True)
         return
     print("bench: generating synthetic weights", file=sys.stderr, flush=True)
     W = syn.moe_weights()

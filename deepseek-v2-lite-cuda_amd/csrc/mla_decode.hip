@@ -290,7 +290,27 @@ __global__ __launch_bounds__(256, 2) void attn_split_kernel(DecodeArgs a) {
   l_lane += __shfl_xor(l_lane, 16, 64);
   l_lane += __shfl_xor(l_lane, 32, 64);
   if (lane < 16) s_l[wave][lane] = l_lane;
-  __syncthreads();
+  __syncthreads();  // also: every wave is past its last read of s_x
+  if (a.n_splits == 1) {
+    // The only split holds every visible key (key 0 among them, so the sum is
+    // >= 1): normalise here and write bf16, staged through s_x for whole-row
+    // stores; no merge pass follows.
+    const float inv = 1.f / ((s_l[0][r16] + s_l[1][r16]) + (s_l[2][r16] + s_l[3][r16]));
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s_x[r16][frag_dim(wave, t, lane, i)] = f32_to_bf16(acc[t][i] * inv);
+    __syncthreads();
+    uint16_t* o = a.out + tok * a.o_tok;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int c = threadIdx.x + 256 * j;  // 16 heads x 256 bf16 pairs
+      const int h = c >> 8, d = (c & 255) * 2;
+      *reinterpret_cast<uint32_t*>(o + h * a.o_head + d) =
+          *reinterpret_cast<const uint32_t*>(&s_x[h][d]);
+    }
+    return;
+  }
   const int64_t part = tok * a.n_splits + split;
   if (threadIdx.x < kHeads) {  // thread t < 16 is lane t of wave 0: head t
     const int h = threadIdx.x;
@@ -405,6 +425,7 @@ extern "C" size_t dsk_mla_decode_workspace_size(int batch, int q_len, int kv_len
   if (batch <= 0 || q_len <= 0 || kv_len <= 0) return 256;
   int S, per;
   split_plan(batch, q_len, kv_len, &S, &per);
+  if (S == 1) return 256;  // one split per token writes the output itself
   const size_t per_token = (size_t)S * (kHeads * kLat + 2 * kHeads) * sizeof(float);
   return align_up((size_t)batch * q_len * per_token, 256);
 }
@@ -471,7 +492,7 @@ extern "C" int dsk_mla_decode_attention(const dsk_bf16* q_abs, int64_t qa_tok, i
   hipStream_t st = as_stream(stream);
   hipLaunchKernelGGL(attn_split_kernel, dim3(S, q_len, batch), dim3(256), 0, st, a);
   int rc = check_launch("attn_split_kernel");
-  if (rc) return rc;
+  if (rc || S == 1) return rc;
   hipLaunchKernelGGL(attn_merge_kernel, dim3(kHeads * kLat / 4 / 16, batch * q_len), dim3(256),
                      0, st, a);
   return check_launch("attn_merge_kernel");

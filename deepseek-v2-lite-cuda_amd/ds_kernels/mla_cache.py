@@ -134,6 +134,39 @@ class AbsorbedMLAWeights:
             w_uv_t=kv[:, nope:].transpose(1, 2).to(torch.bfloat16).contiguous())
 
 
+# A step of at least this many new tokens (a prompt) attends through up-projected
+# K and V, like DeepSeekMLA.forward: the absorbed kernel reads every cached row
+# once per new token, which a long step cannot amortise.
+UP_PROJECTED_MIN_TOKENS = 128
+
+
+def _attend_up_projected(q: torch.Tensor, cache: LatentKVCache, W: MLAWeights, cos: torch.Tensor,
+                         sin: torch.Tensor, eps: float) -> torch.Tensor:
+    """The attention of mla.py:338-384 for the last n of the L cached positions:
+    RMSNorm of the cached latents, kv_b, RoPE of the cached keys and the new
+    queries, bf16 Q.K^T, attn_softmax_ (scale, causal mask offset by L - n, fp32
+    softmax), .V. q: [b, n, h, nope + rope] view of the q projection. Returns
+    bf16 [b, n, h * v_dim]."""
+    b, n, h, _ = q.shape
+    nope, r, vd = W.nope, W.rope_dim, W.v_dim
+    L = cache.current_len
+    lat, pe = cache.get(L)
+    kv = ops.kv_upproj(ops.rms_norm(lat, W.kva_norm, eps), W.kvb).view(b, L, h, nope + vd)
+    kv = kv.transpose(1, 2)                                       # [b, h, L, 256] view
+    cq = cos[L - n:L][None, None].expand(b, 1, n, r)
+    sq = sin[L - n:L][None, None].expand(b, 1, n, r)
+    ck = cos[:L][None, None].expand(b, 1, L, r)
+    sk = sin[:L][None, None].expand(b, 1, L, r)
+    q_rot = ops.rope_single(q[..., nope:].transpose(1, 2), cq, sq)        # [b, h, n, r]
+    k_rot = ops.rope_single(pe[:, None], ck, sk)                          # [b, 1, L, r]
+    qf = torch.cat([q[..., :nope].transpose(1, 2), q_rot], dim=-1)       # [b, h, n, 192]
+    kf = torch.cat([kv[..., :nope], k_rot.expand(b, h, L, r)], dim=-1)   # [b, h, L, 192]
+    scores = torch.matmul(qf, kf.transpose(-1, -2).contiguous())         # bf16 [b, h, n, L]
+    p = ops.attn_softmax_(scores, W.softmax_scale, causal=True)
+    o = torch.matmul(p, kv[..., nope:].contiguous())                      # [b, h, n, v]
+    return o.transpose(1, 2).reshape(b, n, h * vd)
+
+
 def mla_decode_forward(x: torch.Tensor, W: MLAWeights, cache: LatentKVCache, cos: torch.Tensor,
                        sin: torch.Tensor, absorbed: Optional[AbsorbedMLAWeights] = None,
                        eps: float = 1e-6) -> torch.Tensor:
@@ -141,7 +174,10 @@ def mla_decode_forward(x: torch.Tensor, W: MLAWeights, cache: LatentKVCache, cos
     positions cache.current_len .. + n - 1, causal over the cached prefix and
     among themselves. Appends their raw latent and k_pe to the cache and
     returns bf16 [bsz, n, H]. cos/sin: bf16 [positions, rope_dim] tables
-    indexed by position (yarn_cos_sin of at least the final length)."""
+    indexed by position (yarn_cos_sin of at least the final length).
+    Steps of fewer than UP_PROJECTED_MIN_TOKENS tokens use the absorbed
+    attention kernel over the raw cache; longer ones (prompts) up-project the
+    cached latents as the reference forward does."""
     op = "mla_decode_forward"
     ops._req(x.dim() == 3 and x.dtype == torch.bfloat16, f"{op}: x must be bf16 [bsz, n, H].")
     b, n, H = x.shape
@@ -154,6 +190,9 @@ def mla_decode_forward(x: torch.Tensor, W: MLAWeights, cache: LatentKVCache, cos
     kva = ops.linear(x, W.kva)                             # [b, n, 576]
     cache.update(kva[..., :W.kv_lora], kva[..., W.kv_lora:])
     L = cache.current_len
+    if n >= UP_PROJECTED_MIN_TOKENS and L % 8 == 0 and L <= 4096:
+        o = _attend_up_projected(q.view(b, n, h, nope + r), cache, W, cos, sin, eps)
+        return ops.linear(o, W.o)
     q_nope = q[..., :nope].transpose(0, 1).contiguous()    # [h, T, nope]
     q_abs = torch.bmm(q_nope, A.w_uk)                      # [h, T, kv_lora]
     latent, k_pe = cache.get(L)

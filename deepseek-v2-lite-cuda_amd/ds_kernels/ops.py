@@ -460,6 +460,27 @@ def mla_decode_attention(q_abs: torch.Tensor, q_pe: torch.Tensor, latent: torch.
     return out
 
 
+def rope_single(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """The RoPE of `rope` on one tensor x [b, h, s, d] (a strided view with a
+    contiguous last dim) with the pre-indexed cos/sin [b, 1, s, d]; returns a
+    contiguous [b, h, s, d]."""
+    op = "rope"
+    for t in (x, cos, sin):
+        _req(t.is_cuda and t.dtype == torch.bfloat16, f"{op}: inputs must be bf16 CUDA tensors.")
+        _req(t.dim() == 4, f"{op}: inputs must be 4-D.")
+    b, h, s, d = x.shape
+    _req(cos.shape == (b, 1, s, d) and sin.shape == (b, 1, s, d), f"{op}: cos/sin shape incompatible.")
+    if cos.stride(3) != 1 or sin.stride(3) != 1 or cos.stride() != sin.stride():
+        cos, sin = cos.contiguous(), sin.contiguous()
+    sb, sh, ss = _rope_strides(x, "x")
+    out = torch.empty((b, h, s, d), dtype=torch.bfloat16, device=x.device)
+    with torch.cuda.device(x.device):
+        check(lib.dsk_rope(x.data_ptr(), sb, sh, ss, cos.data_ptr(), sin.data_ptr(), cos.stride(0),
+                           cos.stride(2), out.data_ptr(), b, h, s, d,
+                           stream_handle(x.device)), op)
+    return out
+
+
 def rope(q_pe: torch.Tensor, k_pe: torch.Tensor, cos: torch.Tensor,
          sin: torch.Tensor) -> List[torch.Tensor]:
     """Interleaved -> half RoPE on q_pe [b,h,s,d] and k_pe [b,1,s,d] with the

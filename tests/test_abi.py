@@ -105,6 +105,7 @@ def test_mla_decode_validation(dsk):
     ws = lib.dsk_mla_decode_workspace_size(1, 1, 4096)
     assert ws == 64 * (16 * 512 + 32) * 4
     assert lib.dsk_mla_decode_workspace_size(2, 3, 65) == 2 * 3 * 2 * (16 * 512 + 32) * 4
+    assert lib.dsk_mla_decode_workspace_size(1, 600, 4096) == 256  # one split per token: no partials
     # argument order: q_abs, qa_tok, qa_head, q_pe, qp_tok, qp_head, latent, k_pe, ld_tok,
     # ld_batch, cos, sin, eps, scale, batch, q_len, kv_len, out, o_tok, o_head, ws, bytes, stream
     def call(q_len=1, kv_len=64, ld_tok=576, ld_batch=576 * 64, batch=1, qa=(8192, 512),
@@ -121,7 +122,7 @@ def test_mla_decode_validation(dsk):
     assert call(q_abs=None) == 2
     assert call(q_abs=24) == 3
     assert call(out=18) == 3
-    assert call(bytes_=1024) == 5 and "workspace" in _err(dsk)
+    assert call(kv_len=4096, bytes_=1024) == 5 and "workspace" in _err(dsk)
     assert call(batch=256, q_len=256, kv_len=256, ld_batch=576 * 256) == 1 and "65535" in _err(dsk)
 
 

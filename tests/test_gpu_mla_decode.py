@@ -2,9 +2,10 @@
 MLA attention on the raw cached latents, dsk_mla_decode_attention) against the
 oracle's full-sequence DeepSeekMLA.forward (oracle/mla.py mla_forward, fp32,
 causal), whose rows for the positions of the new tokens are what incremental
-decoding must reproduce. Prefix fills, single-token steps, multi-token steps,
-batches, chunk-boundary lengths and the empty-cache start are covered; the
-bar is the bf16 one (max relative error <= 2e-2)."""
+decoding must reproduce. Prefix fills (through the absorbed kernel and, for
+long steps, through up-projected K and V), single-token steps, multi-token
+steps, batches, block-boundary lengths and the empty-cache start are covered;
+the bar is the bf16 one (max relative error <= 2e-2)."""
 import numpy as np
 import pytest
 import torch
@@ -52,7 +53,9 @@ def _run_steps(setup, x, steps):
     (1, [50, 1, 1, 1, 7, 1]),          # prefill, single steps, a multi-token step
     (2, [127, 1, 1, 1]),               # crosses the 64-key chunk boundary at 128
     (2, [63, 2, 64, 1]),
-    (1, [700, 1, 5]),                  # many chunks
+    (1, [700, 1, 5]),                  # many blocks (700 is not a multiple of 8: absorbed kernel)
+    (2, [256, 1, 130]),                # prompt through up-projected K/V, then the kernel (merge)
+    (1, [1, 255, 8]),                  # up-projected step over a one-token prefix
 ])
 def test_decode_matches_full_sequence_oracle(setup, b, steps):
     S = sum(steps)
