@@ -22,6 +22,8 @@ struct GemmArgs {
   int up_row_offset;       // SwiGLU: first up row inside a group's weight
   int max_group_rows;      // upper bound on any group's row count known to the host
                            // (0: unknown, M is used); selects the small-group kernel
+  int64_t a_group_stride;  // skinny kernel: elements between the A bases of consecutive
+  int64_t c_group_stride;  // groups, and of the C bases (0: one base, rows by offsets)
   int b_tiled;             // B stored as MFMA fragments (see the fragment-tiled layout in
                            // dsk.h); ldb is then unused
 };

@@ -981,7 +981,9 @@ __global__ __launch_bounds__(kSkinnyThreads) void skinny_gemm_kernel(GemmArgs p,
   // batch become immediate offsets. Offsets stay below 4 GiB: one group's
   // weights, and at most 64 token rows of A.
   const char* Bg = reinterpret_cast<const char*>(p.B + (int64_t)g * p.b_group_stride);
-  const char* Ab = reinterpret_cast<const char*>(p.A);
+  // per-group bases of A and C (batched products: groups of M rows each)
+  const char* Ab = reinterpret_cast<const char*>(p.A + (int64_t)g * p.a_group_stride);
+  uint16_t* const Cg = p.C + (int64_t)g * p.c_group_stride;
   // K steps (of 16) of this wave: an even split of K/16 over the waves
   const int ksteps = p.K / 16;
   const int s_beg = wave * ksteps / kSkinnyWaves;
@@ -1153,7 +1155,7 @@ __global__ __launch_bounds__(kSkinnyThreads) void skinny_gemm_kernel(GemmArgs p,
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const int m = m0 + mt * 32 + r32;
-        uint16_t* crow = p.C + (int64_t)m * p.ldc;
+        uint16_t* crow = Cg + (int64_t)m * p.ldc;
         constexpr int JN = SWIGLU ? 1 : NB;
 #pragma unroll
         for (int j = 0; j < JN; ++j) {
@@ -1275,7 +1277,8 @@ static int launch_wide_gemm(const GemmArgs& a, hipStream_t st) {
 
 template <int MT, bool SWIGLU, bool GATHER, bool TILED>
 static int launch_skinny_gemm(const GemmArgs& a, hipStream_t st) {
-  const int G = a.offsets != nullptr ? a.G : 1;
+  // groups: by offsets, or a batch of G equal groups of M rows (per-group bases)
+  const int G = a.offsets != nullptr || a.a_group_stride != 0 || a.c_group_stride != 0 ? a.G : 1;
   const int n_blocks = SWIGLU ? (a.N + 31) / 32 : (a.N + 63) / 64;
   const int64_t grid = (int64_t)G * n_blocks;
   hipLaunchKernelGGL((skinny_gemm_kernel<MT, SWIGLU, GATHER, TILED>), dim3((unsigned)grid),
@@ -1467,6 +1470,37 @@ extern "C" int dsk_linear_ex(const dsk_bf16* x, int64_t ld_x, const dsk_bf16* w,
   int rc = validate_gemm(a, "linear");
   if (rc) return rc;
   DSK_REQUIRE(ld_out >= N, DSK_ERR_INVALID_ARG, "linear: ld_out < N");
+  return run_gemm(a, false, as_stream(stream));
+}
+
+extern "C" int dsk_linear_batched(const dsk_bf16* x, int64_t ld_x, int64_t x_batch_stride,
+                                  const dsk_bf16* w_tiled, dsk_bf16* out, int64_t ld_out,
+                                  int64_t out_batch_stride, int batch, int M, int K, int N,
+                                  void* stream) {
+  DSK_REQUIRE(batch >= 0 && M >= 0, DSK_ERR_INVALID_ARG, "linear_batched: batch and M >= 0");
+  if (batch == 0 || M == 0) return DSK_OK;
+  DSK_REQUIRE(batch <= 65535 && M <= kSkinnyMaxRows, DSK_ERR_INVALID_ARG,
+              "linear_batched: needs M <= 64 rows per batch entry and batch <= 65535");
+  DSK_REQUIRE(x_batch_stride % 8 == 0 && out_batch_stride % 4 == 0, DSK_ERR_ALIGNMENT,
+              "linear_batched: batch strides must keep rows aligned (x: 16 B, out: 8 B)");
+  DSK_REQUIRE(x_batch_stride >= 0 && out_batch_stride >= 0 &&
+                  (batch == 1 || (x_batch_stride > 0 && out_batch_stride > 0)),
+              DSK_ERR_INVALID_ARG, "linear_batched: batch strides must be positive");
+  GemmArgs a{};
+  a.A = x; a.lda = ld_x; a.a_group_stride = x_batch_stride;
+  a.B = w_tiled; a.ldb = K; a.b_group_stride = (int64_t)N * K;
+  a.C = out; a.ldc = ld_out; a.c_group_stride = out_batch_stride;
+  a.offsets = nullptr; a.G = batch;
+  a.M = M; a.N = N; a.K = K;
+  a.max_group_rows = M;
+  a.b_tiled = 1;
+  int rc = validate_gemm(a, "linear_batched");
+  if (rc) return rc;
+  DSK_REQUIRE(ld_out >= N, DSK_ERR_INVALID_ARG, "linear_batched: ld_out < N");
+  // 32-bit byte offsets inside each entry (rows of A and C are addressed from
+  // the entry's base)
+  DSK_REQUIRE((int64_t)M * ld_x * 2 <= (int64_t)UINT32_MAX, DSK_ERR_INVALID_ARG,
+              "linear_batched: an entry of x spans more than 4 GiB");
   return run_gemm(a, false, as_stream(stream));
 }
 

@@ -25,7 +25,7 @@ from typing import Optional, Tuple
 import torch
 
 from . import ops
-from .expert_prepack import untile_weights
+from .expert_prepack import tile_weights, untile_weights
 from .mla import MLAWeights
 
 
@@ -89,6 +89,18 @@ class LatentKVCache:
         self.k_pe_cache[:, slot, :] = k_pe.to(self.device, self.dtype)
         self._len += n
 
+    def append_slots(self, n: int) -> torch.Tensor:
+        """Reserve the next n token slots and return them as a [bsz, n, 576] view of
+        the cache rows (raw latent, then raw RoPE key), for a producer that writes
+        them in place (the kv_a projection of a decode step). Same overflow error as
+        `update`; not part of the reference API."""
+        if self._len + n > self.max_seq:
+            raise RuntimeError(f"KV cache overflow: current_len={self._len}, new_tokens={n}, "
+                               f"max_seq={self.max_seq}. Increase max_seq or reset the cache.")
+        rows = self.rows[:, self._len:self._len + n]
+        self._len += n
+        return rows
+
     def get(self, seq_len: Optional[int] = None) -> Tuple[torch.Tensor, torch.Tensor]:
         """Views of the first seq_len tokens (default: all stored), mla_cache.py:145-169.
         ValueError if more tokens are asked for than are stored."""
@@ -120,18 +132,26 @@ class LatentKVCache:
 class AbsorbedMLAWeights:
     """kv_b folded for the absorbed form, with the latent RMSNorm weight w in it:
     w_uk[h] = W_UK[h] * w (the k_nope rows of head h, [nope, kv_lora]) and
-    w_uv_t[h] = (W_UV[h] * w)^T ([kv_lora, v_dim]); both bf16, contiguous."""
+    w_uv_t[h] = (W_UV[h] * w)^T ([kv_lora, v_dim]), bf16 contiguous for torch's
+    batched products; and the same two per-head matrices in the operand order
+    and fragment-tiled layout of `linear_batched`: uk_tiled = tile of the
+    [16, kv_lora, nope] stack w_uk^T, uv_tiled = tile of [16, v_dim, kv_lora]."""
     w_uk: torch.Tensor
     w_uv_t: torch.Tensor
+    uk_tiled: Optional[torch.Tensor] = None
+    uv_tiled: Optional[torch.Tensor] = None
 
     @staticmethod
     def from_mla(W: MLAWeights) -> "AbsorbedMLAWeights":
         kvb = W.kvb if W.kvb.dim() == 2 else untile_weights(W.kvb[None])[0]
         h, nope, vd = W.n_heads, W.nope, W.v_dim
         kv = kvb.float().view(h, nope + vd, W.kv_lora) * W.kva_norm.float()[None, None, :]
+        uk = kv[:, :nope].to(torch.bfloat16)        # [h, nope, lora]
+        uv = kv[:, nope:].to(torch.bfloat16)        # [h, v, lora]
         return AbsorbedMLAWeights(
-            w_uk=kv[:, :nope].to(torch.bfloat16).contiguous(),
-            w_uv_t=kv[:, nope:].transpose(1, 2).to(torch.bfloat16).contiguous())
+            w_uk=uk.contiguous(), w_uv_t=uv.transpose(1, 2).contiguous(),
+            uk_tiled=tile_weights(uk.transpose(1, 2).contiguous()),
+            uv_tiled=tile_weights(uv.contiguous()))
 
 
 # A step of at least this many new tokens (a prompt) attends through up-projected
@@ -185,20 +205,31 @@ def mla_decode_forward(x: torch.Tensor, W: MLAWeights, cache: LatentKVCache, cos
     ops._req(cache.kv_lora_rank == W.kv_lora and cache.rope_head_dim == W.rope_dim,
              f"{op}: cache widths do not match the weights.")
     A = absorbed if absorbed is not None else AbsorbedMLAWeights.from_mla(W)
-    h, nope, r = W.n_heads, W.nope, W.rope_dim
-    q = ops.linear(x, W.q).view(b * n, h, nope + r)      # [T, h, 192]
-    kva = ops.linear(x, W.kva)                             # [b, n, 576]
-    cache.update(kva[..., :W.kv_lora], kva[..., W.kv_lora:])
+    h, nope, r, vd, lora = W.n_heads, W.nope, W.rope_dim, W.v_dim, W.kv_lora
+    T = b * n
+    q = ops.linear(x, W.q).view(T, h, nope + r)           # [T, h, 192]
+    x2 = x.reshape(T, H)
+    rows = cache.append_slots(n)                           # [b, n, 576] slots
+    if b == 1 or n == 1:                                   # one row stride: project in place
+        ops.linear(x2, W.kva, out=rows[0] if b == 1 else rows[:, 0])
+    else:
+        rows.copy_(ops.linear(x2, W.kva).view(b, n, lora + r))
     L = cache.current_len
     if n >= UP_PROJECTED_MIN_TOKENS and L % 8 == 0 and L <= 4096:
         o = _attend_up_projected(q.view(b, n, h, nope + r), cache, W, cos, sin, eps)
         return ops.linear(o, W.o)
-    q_nope = q[..., :nope].transpose(0, 1).contiguous()    # [h, T, nope]
-    q_abs = torch.bmm(q_nope, A.w_uk)                      # [h, T, kv_lora]
     latent, k_pe = cache.get(L)
-    o_lat = torch.empty((h, b * n, W.kv_lora), dtype=torch.bfloat16, device=x.device)
+    small = T <= 64 and A.uk_tiled is not None
+    if small:   # per-head products on strided views, one launch each
+        q_abs = ops.linear_batched(q[..., :nope].transpose(0, 1), A.uk_tiled)  # [h, T, lora]
+    else:
+        q_abs = torch.bmm(q[..., :nope].transpose(0, 1).contiguous(), A.w_uk)
+    o_lat = torch.empty((h, T, lora), dtype=torch.bfloat16, device=x.device)
     ops.mla_decode_attention(q_abs.transpose(0, 1), q[..., nope:], latent, k_pe, cos, sin,
                              W.softmax_scale, eps, out=o_lat.transpose(0, 1))
-    o = torch.bmm(o_lat, A.w_uv_t)                         # [h, T, v_dim]
-    o = o.transpose(0, 1).reshape(b, n, h * W.v_dim)
-    return ops.linear(o, W.o)
+    if small:   # o[t, h*v:(h+1)*v] = o_lat[h, t] @ (W_UV[h] * w)^T, written token-major
+        o = torch.empty((T, h * vd), dtype=torch.bfloat16, device=x.device)
+        ops.linear_batched(o_lat, A.uv_tiled, out=o.view(T, h, vd).transpose(0, 1))
+    else:
+        o = torch.bmm(o_lat, A.w_uv_t).transpose(0, 1).reshape(T, h * vd)
+    return ops.linear(o, W.o).view(b, n, -1)

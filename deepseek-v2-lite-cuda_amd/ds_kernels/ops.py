@@ -278,11 +278,13 @@ def moe_gemm2(swiglu_out: torch.Tensor, w2: torch.Tensor,
     return out
 
 
-def linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+def linear(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor = None) -> torch.Tensor:
     """x[..., K] @ weight[N, K]^T with the MFMA GEMM (bf16 in/out, fp32 acc).
     x may be a row-strided view (last dim contiguous, row stride % 8 == 0).
     weight is [N, K] row-major, or fragment-tiled [N/32, K/16, 64, 8]
-    (tile_weights(w[None])[0]), which runs the weight-streaming kernel."""
+    (tile_weights(w[None])[0]), which runs the weight-streaming kernel.
+    out: optional [M, N] bf16 destination with a contiguous last dim and any row
+    stride (e.g. rows of a cache); returned as given."""
     op = "linear"
     _req(x.is_cuda and weight.is_cuda, f"{op}: tensors must be CUDA tensors.")
     _req(x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16, f"{op}: bfloat16 only.")
@@ -300,13 +302,45 @@ def linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     x2 = x.reshape(-1, K) if not x.is_contiguous() or x.dim() != 2 else x
     _req(x2.stride(-1) == 1, f"{op}: last dim of x must be contiguous.")
     M = x2.shape[0]
-    out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    given = out is not None
+    if given:
+        _req(out.is_cuda and out.dtype == torch.bfloat16 and out.dim() == 2 and
+             tuple(out.shape) == (M, N) and out.stride(1) == 1,
+             f"{op}: out must be bf16 [{M}, {N}] with a contiguous last dim.")
+    else:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
     if M:
         with torch.cuda.device(x.device):
             check(lib.dsk_linear_ex(x2.data_ptr(), x2.stride(0), weight.data_ptr(),
-                                    1 if tiled else 0, out.data_ptr(), N, M, K, N,
+                                    1 if tiled else 0, out.data_ptr(), out.stride(0), M, K, N,
                                     stream_handle(x.device)), op)
-    return out.view(*x.shape[:-1], N)
+    return out if given else out.view(*x.shape[:-1], N)
+
+
+def linear_batched(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor = None) -> torch.Tensor:
+    """out[b] = x[b] @ weight[b]^T for every entry b of a batch, in one launch
+    (dsk_linear_batched), up to 64 rows per entry. x: bf16 [batch, M, K], any
+    strides with a contiguous last dim; weight: fragment-tiled [batch, N/32,
+    K/16, 64, 8] (tile_weights of a [batch, N, K] stack); out: optional [batch,
+    M, N] destination view. Returns out."""
+    op = "linear_batched"
+    _req(x.is_cuda and x.dtype == torch.bfloat16 and x.dim() == 3 and x.stride(2) == 1,
+         f"{op}: x must be a bf16 CUDA tensor [batch, M, K] with a contiguous last dim.")
+    nb, M, K = x.shape
+    _req(weight.is_cuda and weight.is_contiguous() and weight.dtype == torch.bfloat16 and
+         weight.dim() == 5 and weight.shape[0] == nb and tuple(weight.shape[3:]) == (64, 8) and
+         weight.shape[2] * 16 == K, f"{op}: weight must be tiled [{nb}, N/32, {K // 16}, 64, 8].")
+    N = weight.shape[1] * 32
+    if out is None:
+        out = torch.empty((nb, M, N), dtype=torch.bfloat16, device=x.device)
+    _req(out.is_cuda and out.dtype == torch.bfloat16 and tuple(out.shape) == (nb, M, N) and
+         out.stride(2) == 1, f"{op}: out must be bf16 [{nb}, {M}, {N}] with a contiguous last dim.")
+    if nb and M:
+        with torch.cuda.device(x.device):
+            check(lib.dsk_linear_batched(x.data_ptr(), x.stride(1), x.stride(0), weight.data_ptr(),
+                                         out.data_ptr(), out.stride(1), out.stride(0), nb, M, K,
+                                         N, stream_handle(x.device)), op)
+    return out
 
 
 def kv_upproj(normed_kv: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:

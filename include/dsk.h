@@ -212,6 +212,20 @@ int dsk_rope_qk(const dsk_bf16* q, int64_t qsb, int64_t qsh, int64_t qss,
                 int64_t cs, dsk_bf16* q_out, dsk_bf16* k_out, int B, int Hq,
                 int Hk, int S, int d, void* stream);
 
+/* --------------------------------------------------------- batched linear --
+ * out[b] = x[b] @ w[b]^T for b < batch, with M <= 64 rows per entry (the
+ * weight-streaming small-group kernel; one launch for all entries). Entry b of
+ * x starts x_batch_stride elements after entry b-1 and has rows ld_x apart;
+ * out likewise with out_batch_stride and ld_out; w is fragment-tiled
+ * [batch, N/32, K/16, 64, 8]. Runs the per-head products of absorbed MLA
+ * decode (q_nope[h] -> q_abs[h] and o_lat[h] -> o[h], 16 entries) on strided
+ * views, replacing a transpose copy and a torch batched product each; the
+ * reference has no counterpart (it up-projects K and V instead). */
+int dsk_linear_batched(const dsk_bf16* x, int64_t ld_x, int64_t x_batch_stride,
+                       const dsk_bf16* w_tiled, dsk_bf16* out, int64_t ld_out,
+                       int64_t out_batch_stride, int batch, int M, int K, int N,
+                       void* stream);
+
 /* ------------------------------------------------------ attention softmax --
  * In place over bf16 attention scores [rows, kv_len] (row stride ld): the
  * eager sequence of DeepSeekMLA.forward (mla.py:366-381) in one pass,

@@ -126,6 +126,20 @@ def test_mla_decode_validation(dsk):
     assert call(batch=256, q_len=256, kv_len=256, ld_batch=576 * 256) == 1 and "65535" in _err(dsk)
 
 
+def test_linear_batched_validation(dsk):
+    lib = dsk.lib
+    # x, ld_x, x_batch_stride, w, out, ld_out, out_batch_stride, batch, M, K, N, stream
+    rc = lib.dsk_linear_batched(16, 3072, 192, 16, 16, 2048, 128, 16, 65, 128, 512, None)
+    assert rc == 1 and "64" in _err(dsk)
+    rc = lib.dsk_linear_batched(16, 3072, 190, 16, 16, 2048, 128, 16, 1, 128, 512, None)
+    assert rc == 3
+    rc = lib.dsk_linear_batched(16, 3072, 0, 16, 16, 2048, 128, 16, 1, 128, 512, None)
+    assert rc == 1 and "positive" in _err(dsk)
+    rc = lib.dsk_linear_batched(16, 3072, 192, 16, 16, 2048, 128, 16, 1, 100, 512, None)
+    assert rc == 1
+    assert lib.dsk_linear_batched(None, 0, 0, None, None, 0, 0, 0, 1, 128, 512, None) == 0
+
+
 def test_norm_rope_validation(dsk):
     lib = dsk.lib
     rc = lib.dsk_rms_norm(16, 511, 16, 16, 511, 4, 511, 1e-6, None)

@@ -120,3 +120,21 @@ def test_decode_op_rejects_bad_shapes(setup):
     with pytest.raises(RuntimeError, match="cos/sin"):
         dsk.mla_decode_attention(q_abs[:2], q_pe[:2], rows[..., :512], rows[..., 512:],
                                  cos[:4], sin[:4], 0.1)
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 128, 512), (5, 128, 512), (64, 512, 128), (3, 512, 128)])
+def test_linear_batched_strided_views(setup, M, K, N):
+    """The per-head products of the decode step: 16 entries on strided views (the
+    q_nope slice of the q projection in, a token-major output slice out),
+    against an fp32 reference of the same bf16 operands."""
+    dsk = setup[0]
+    g = torch.Generator().manual_seed(M * 7 + K)
+    big = torch.randn(M, 16, K + 64, generator=g).to(torch.bfloat16)   # [tokens, heads, K + pad]
+    w = (torch.randn(16, N, K, generator=g) * 0.05).to(torch.bfloat16)
+    x = big.to(DEV)[..., :K].transpose(0, 1)                            # [16, M, K] strided
+    out_full = torch.zeros(M, 16, N + 8, dtype=torch.bfloat16, device=DEV)
+    out = out_full[..., :N].transpose(0, 1)                              # [16, M, N] strided
+    dsk.linear_batched(x, dsk.tile_weights(w.to(DEV)), out=out)
+    ref = torch.einsum("hmk,hnk->hmn", big[..., :K].transpose(0, 1).float(), w.float())
+    assert max_rel_err(np32(out), ref.numpy()) <= BF16_TOL
+    assert torch.count_nonzero(out_full[..., N:]) == 0   # nothing written past the slice

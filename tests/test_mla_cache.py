@@ -83,3 +83,17 @@ def test_reset_keeps_buffers_and_repr_counts_used_tokens():
     assert "tokens=512/1024, used=1.12MB/2.25MB" in repr(c)
     c.reset()
     assert c.current_len == 0 and c.remaining_capacity == 1024 and c.rows.data_ptr() == ptr
+
+
+def test_append_slots_reserves_views_in_order():
+    c = LatentKVCache(2, 6, device="cpu")
+    c.update(_tokens(2, 2, 0, 512), _tokens(2, 2, 1, 64))
+    rows = c.append_slots(3)
+    assert rows.shape == (2, 3, 576) and c.current_len == 5
+    rows.copy_(_tokens(2, 3, 2, 576))
+    lat, pe = c.get()
+    assert torch.equal(lat[:, 2:], rows[..., :512]) and torch.equal(pe[:, 2:], rows[..., 512:])
+    assert rows.data_ptr() == c.rows[:, 2:].data_ptr()
+    with pytest.raises(RuntimeError, match="KV cache overflow: current_len=5, new_tokens=2"):
+        c.append_slots(2)
+    assert c.current_len == 5
