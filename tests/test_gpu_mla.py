@@ -229,3 +229,40 @@ def test_decoder_layer_matches_oracle(mla_setup):
     ref = ol.decoder_layer(np32(x), p)
     assert out.shape == (b, s, 2048)
     assert max_rel_err(np32(out), ref) <= BF16_TOL
+
+
+def test_config3_projection_block_full_size(mla_setup):
+    """BASELINE config 3 at its full size (b=8, s=2048): every output of the
+    projection block against the oracle."""
+    dm, w, W, wn = mla_setup
+    b, s = 8, 2048
+    g = torch.Generator().manual_seed(31)
+    x = torch.randn(b, s, 2048, generator=g).to(torch.bfloat16)
+    cos, sin = dm.yarn_cos_sin(s)
+    outs = dm.mla_projections(x.to(DEV), W, cos.to(DEV), sin.to(DEV))
+    refs = ol.mla_projections(np32(x), wn["q"], wn["kva"], wn["kva_norm"], wn["kvb"], _bf(cos),
+                              _bf(sin))
+    for name, o, r in zip(["q_nope", "q_rot", "k_nope", "v", "k_rot", "latent"], outs, refs):
+        assert max_rel_err(np32(o), r) <= BF16_TOL, name
+
+
+def test_config4_decoder_layer_full_size_properties(mla_setup):
+    """BASELINE config 4 at its full size (b=4, s=2048), through properties that
+    hold at any size: the layer is deterministic (two runs bit-identical), its
+    output is finite, and each sequence's rows match the layer run on that
+    sequence alone (attention never mixes sequences; routing is per token)."""
+    dm, w, W, wn = mla_setup
+    from ds_kernels import synthetic as syn
+    P = dm.DecoderLayerWeights.from_tensors(w, syn.moe_weights(), torch.device(DEV))
+    b, s = 4, 2048
+    g = torch.Generator().manual_seed(41)
+    x = torch.randn(b, s, 2048, generator=g).to(torch.bfloat16).to(DEV)
+    cos, sin = dm.yarn_cos_sin(s, device=DEV)
+    out1 = dm.decoder_layer_forward(x, P, cos, sin)
+    out2 = dm.decoder_layer_forward(x, P, cos, sin)
+    torch.cuda.synchronize()
+    assert torch.equal(out1, out2)
+    assert torch.isfinite(out1.float()).all()
+    one = dm.decoder_layer_forward(x[2:3].contiguous(), P, cos, sin)
+    torch.cuda.synchronize()
+    assert max_rel_err(np32(one), np32(out1[2:3])) <= BF16_TOL
