@@ -503,39 +503,62 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void grouped_gemm_kernel
 
     // ---- epilogue (the next tile's first stages are already in flight):
     // lane owns token row m = ... + (lane & 31) and 4 consecutive output
-    // columns per 4-register group
+    // columns per 4-register group; lanes l and l + 32 hold the same row.
+    // One lane-half swap per pair of groups gives lane l columns 0-7 and
+    // lane l + 32 columns 8-15 of a 16-column run, so each store instruction
+    // writes 16 contiguous bytes per row instead of 8.
     {
       constexpr int JN = SWIGLU ? TN / 2 : TN;
       constexpr int WOUT = SWIGLU ? WN / 2 : WN;
+      const bool vec16 = (reinterpret_cast<uintptr_t>(p.C) & 15) == 0 && (p.ldc & 7) == 0;
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         if (i >= tma) continue;
         const int m = ct.m0 + wave_m * WM + 32 * i + (lane & 31);
-        if (m >= ct.me) continue;
+        if (m >= ct.me) continue;  // the same for lanes l and l + 32
         uint16_t* crow = p.C + (int64_t)m * p.ldc;
 #pragma unroll
         for (int j = 0; j < JN; ++j) {
 #pragma unroll
-          for (int qg = 0; qg < 4; ++qg) {
-            const int nb = ct.n0 + wave_n * WOUT + 32 * j + 8 * qg + 4 * (lane >> 5);
-            float v[4];
+          for (int q2 = 0; q2 < 2; ++q2) {
+            uint32_t w[2][2];  // [group 2*q2 + h][packed column pair]
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-              if constexpr (SWIGLU)
-                v[c] = silu_f(acc_read(acc[j][i][4 * qg + c])) *
-                       acc_read(acc[j + TN / 2][i][4 * qg + c]);
-              else
-                v[c] = acc_read(acc[j][i][4 * qg + c]);
+            for (int h = 0; h < 2; ++h) {
+              const int qg = 2 * q2 + h;
+              float v[4];
+#pragma unroll
+              for (int c = 0; c < 4; ++c) {
+                if constexpr (SWIGLU)
+                  v[c] = silu_f(acc_read(acc[j][i][4 * qg + c])) *
+                         acc_read(acc[j + TN / 2][i][4 * qg + c]);
+                else
+                  v[c] = acc_read(acc[j][i][4 * qg + c]);
+              }
+              w[h][0] = pack_bf16x2(v[0], v[1]);
+              w[h][1] = pack_bf16x2(v[2], v[3]);
             }
-            if (nb + 3 < p.N) {
-              u32x2_t o;
-              o[0] = pack_bf16x2(v[0], v[1]);
-              o[1] = pack_bf16x2(v[2], v[3]);
-              *reinterpret_cast<u32x2_t*>(crow + nb) = o;
+            // upper lanes of w[0] <-> lower lanes of w[1]
+#pragma unroll
+            for (int d = 0; d < 2; ++d) {
+              const auto r = __builtin_amdgcn_permlane32_swap(w[0][d], w[1][d], false, false);
+              w[0][d] = r[0];
+              w[1][d] = r[1];
+            }
+            const int nb = ct.n0 + wave_n * WOUT + 32 * j + 16 * q2 + 8 * (lane >> 5);
+            if (nb + 7 < p.N) {
+              if (vec16) {
+                const u32x4_t o = {w[0][0], w[0][1], w[1][0], w[1][1]};
+                *reinterpret_cast<u32x4_t*>(crow + nb) = o;
+              } else {
+                const u32x2_t lo = {w[0][0], w[0][1]}, hi = {w[1][0], w[1][1]};
+                *reinterpret_cast<u32x2_t*>(crow + nb) = lo;
+                *reinterpret_cast<u32x2_t*>(crow + nb + 4) = hi;
+              }
             } else {
 #pragma unroll
-              for (int c = 0; c < 4; ++c)
-                if (nb + c < p.N) crow[nb + c] = f32_to_bf16(v[c]);
+              for (int c = 0; c < 8; ++c)
+                if (nb + c < p.N)
+                  crow[nb + c] = static_cast<uint16_t>(w[c >> 2][(c >> 1) & 1] >> (16 * (c & 1)));
             }
           }
         }
