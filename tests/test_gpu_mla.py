@@ -104,6 +104,24 @@ def test_linear(dsk, M, K, N):
     assert max_rel_err(np32(out), ref) <= BF16_TOL
 
 
+@pytest.mark.parametrize("N,ld_out", [(200, 216), (200, 204), (136, 140), (1000, 1000)])
+def test_linear_strided_output_rows(dsk, N, ld_out):
+    """The 256-row tile kernel's row stores into an output view whose row
+    pitch is ld_out: 16-byte stores when the pitch is a multiple of 8
+    elements, 8-byte stores otherwise, and a per-element tail when N is not
+    a multiple of 16. Columns N .. ld_out-1 must stay untouched."""
+    M, K = 300, 256
+    g = torch.Generator().manual_seed(N + ld_out)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    full = torch.full((M, ld_out), 7.0, dtype=torch.bfloat16, device=DEV)
+    out = full[:, :N]
+    dsk.linear(x.to(DEV), w.to(DEV), out=out)
+    torch.cuda.synchronize()
+    assert max_rel_err(np32(out), np32(x) @ np32(w).T) <= BF16_TOL
+    assert bool((full[:, N:] == 7.0).all())
+
+
 @pytest.mark.parametrize("M,K,N", [(8, 2048, 3072), (130, 2048, 576), (1000, 512, 4096),
                                    (300, 2048, 2048), (77, 128, 96), (50, 192, 64)])
 def test_linear_tiled_weight(dsk, M, K, N):
