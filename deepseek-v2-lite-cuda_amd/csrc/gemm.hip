@@ -48,6 +48,7 @@
 #include "dsk_internal.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <cstdio>
 #include <mutex>
 #include <type_traits>
@@ -1231,18 +1232,37 @@ __global__ __launch_bounds__(256) void zero_uncovered_rows_kernel(
 }
 
 // ------------------------------------------------------------------ host ----
-static int num_cus() {
-  static int cached[64] = {0};
+constexpr int kMaxDevices = 64;
+
+// The device the calling thread has current, or -1 outside [0, kMaxDevices).
+static int current_device() {
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
+  return hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices ? dev : -1;
+}
+
+// CU count of the current device, queried once per device (any thread).
+static int num_cus() {
+  static std::atomic<int> cached[kMaxDevices];  // static storage: starts at 0
+  const int dev = current_device();
+  if (dev < 0) return 256;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         n <= 0)
       n = 256;
-    cached[dev] = n;
+    cached[dev].store(n, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return n;
+}
+
+// Raises a kernel's dynamic LDS limit on the current device; `once` is the
+// caller's per-kernel flag array, one flag per device.
+static void allow_lds(std::once_flag (&once)[kMaxDevices], const void* kern, int bytes) {
+  const int dev = current_device();
+  if (dev < 0) return;
+  std::call_once(once[dev], [&] {
+    (void)hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  });
 }
 
 template <int BM, int BN, int WAVES_M, int WAVES_N, int BK, int STAGES, bool SWIGLU,
@@ -1250,11 +1270,8 @@ template <int BM, int BN, int WAVES_M, int WAVES_N, int BK, int STAGES, bool SWI
 static int launch_grouped_gemm(const GemmArgs& a, hipStream_t st) {
   using Cfg = GemmCfg<BM, BN, WAVES_M, WAVES_N, BK, STAGES, SWIGLU>;
   auto kern = grouped_gemm_kernel<BM, BN, WAVES_M, WAVES_N, BK, STAGES, SWIGLU, GATHER, TILED>;
-  static std::once_flag once;
-  std::call_once(once, [&] {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::LDS_BYTES);
-  });
+  static std::once_flag once[kMaxDevices];
+  allow_lds(once, reinterpret_cast<const void*>(kern), Cfg::LDS_BYTES);
   const int G = a.offsets != nullptr ? a.G : 1;
   const int64_t nt = (a.N + Cfg::OUT_N - 1) / Cfg::OUT_N;
   const int64_t upper = ((int64_t)(a.M + BM - 1) / BM + (a.offsets ? G : 0)) * nt;
@@ -1276,11 +1293,8 @@ static int launch_grouped_gemm(const GemmArgs& a, hipStream_t st) {
 template <bool SWIGLU, bool GATHER>
 static int launch_wide_gemm(const GemmArgs& a, hipStream_t st) {
   auto kern = wide_gemm_kernel<SWIGLU, GATHER>;
-  static std::once_flag once;
-  std::call_once(once, [&] {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kWideLdsBytes);
-  });
+  static std::once_flag once[kMaxDevices];
+  allow_lds(once, reinterpret_cast<const void*>(kern), kWideLdsBytes);
   constexpr int OUT_N = SWIGLU ? 32 * kWideWaves : 64 * kWideWaves;
   const int G = a.offsets != nullptr ? a.G : 1;
   const int64_t nt = (a.N + OUT_N - 1) / OUT_N;

@@ -43,6 +43,32 @@ def _err(dsk):
     return dsk.lib.dsk_last_error().decode()
 
 
+def test_error_text_is_per_thread(dsk):
+    """dsk_last_error() is thread-local: two threads failing different checks at the
+    same time each read their own message (ctypes releases the GIL around calls)."""
+    import threading
+    lib = dsk.lib
+    seen = {0: set(), 1: set()}
+
+    def worker(i):
+        for _ in range(300):
+            if i == 0:
+                rc = lib.dsk_moe_routing(None, 65, None, None, 8, 4, 65, 6, None, 0, None)
+            else:
+                rc = lib.dsk_moe_routing(None, 64, None, None, 8, 4, 64, 7, None, 0, None)
+            seen[i].add((rc, lib.dsk_last_error().decode()))
+
+    th = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join()
+    assert len(seen[0]) == 1 and len(seen[1]) == 1
+    (rc0, m0), = seen[0]
+    (rc1, m1), = seen[1]
+    assert rc0 == rc1 == 1 and "num_experts" in m0 and "top_k" in m1
+
+
 def test_routing_limits_rejected(dsk):
     lib = dsk.lib
     rc = lib.dsk_moe_routing(None, 65, None, None, 8, 4, 65, 6, None, 0, None)

@@ -397,3 +397,40 @@ def test_op_pipeline_matches_fused(dsk, full_layer):
     ref = _oracle_layer(Wn, x, lg, 6, shared=False)
     for o in (out, out_f, fused):
         assert max_rel_err(np32(o), ref) <= BF16_TOL
+
+
+def test_concurrent_calls_on_two_streams(dsk, full_layer, tiled_layer):
+    """The library keeps no per-call global state (thread-local error text and
+    per-device caches only), so calls from two host threads, each on its own
+    stream, run side by side. Each thread runs the fused layer 4 times (T = 16 and
+    T = 4096); every result equals the single-threaded one bit for bit."""
+    import threading
+    from ds_kernels import synthetic as syn
+    W, _, _, nsh, _ = full_layer
+    w1, w2 = tiled_layer
+    wgd = dsk.tile_weights(W.wg.to(torch.bfloat16)[None])[0].to(DEV)
+    xs = [syn.tokens(T, seed=s).to(torch.bfloat16).to(DEV) for T, s in ((16, 1), (4096, 2))]
+    ref = [dsk.moe_layer_forward(x, wgd, w1, w2, 6, nsh) for x in xs]
+    torch.cuda.synchronize()
+    results = [[None] * 4 for _ in xs]
+    errors = []
+
+    def worker(i):
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                for r in range(4):
+                    results[i][r] = dsk.moe_layer_forward(xs[i], wgd, w1, w2, 6, nsh)
+            s.synchronize()
+        except Exception as e:  # handed to the main thread
+            errors.append(e)
+
+    th = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join(timeout=60)
+    assert not errors, errors
+    for i in range(2):
+        for r in range(4):
+            assert torch.equal(results[i][r], ref[i]), (i, r)
