@@ -73,6 +73,9 @@ class MLAWeights:
     kva_norm: torch.Tensor   # [kv_lora] fp32
     kvb: torch.Tensor        # [heads*(nope+v), kv_lora]
     o: torch.Tensor          # [H, heads*v]
+    # optional [q rows; kva rows] in one matrix (q and kva then view into it),
+    # so that the prefill projections run as one GEMM launch
+    q_kva: Optional[torch.Tensor] = None
     n_heads: int = 16
     nope: int = 128
     rope_dim: int = 64
@@ -87,9 +90,14 @@ class MLAWeights:
         def bf(t):
             t = t.to(device=device, dtype=torch.bfloat16).contiguous()
             return tile_weights(t[None])[0] if tiled else t
-        return MLAWeights(q=bf(w["q"]), kva=bf(w["kva"]),
+        # q and kva share one matrix: the tiled layout keeps 32-row blocks in
+        # order along its first dimension, so both are leading-dim slices of it
+        nq = w["q"].shape[0]
+        q_kva = bf(torch.cat([w["q"], w["kva"]]))
+        split = nq // 32 if tiled else nq
+        return MLAWeights(q=q_kva[:split], kva=q_kva[split:],
                           kva_norm=w["kva_norm"].to(device=device, dtype=torch.float32),
-                          kvb=bf(w["kvb"]), o=bf(w["o"]))
+                          kvb=bf(w["kvb"]), o=bf(w["o"]), q_kva=q_kva)
 
     @property
     def softmax_scale(self) -> float:
@@ -108,8 +116,15 @@ def mla_projections(x: torch.Tensor, W: MLAWeights, cos: torch.Tensor, sin: torc
     and v are strided views of the projection outputs."""
     b, s, _ = x.shape
     h, nope, r, vd, lora = W.n_heads, W.nope, W.rope_dim, W.v_dim, W.kv_lora
-    q = ops.linear(x, W.q).view(b, s, h, nope + r).transpose(1, 2)     # [b,h,s,192] view
-    kva = ops.linear(x, W.kva)                                         # [b,s,576]
+    nq = h * (nope + r)
+    if W.q_kva is not None:
+        # one GEMM for both projections (q_proj alone leaves no partial round of
+        # tiles for kv_a's 576 columns to fill); q and kva are column slices
+        y = ops.linear(x, W.q_kva)                                     # [b,s,3072+576]
+        q, kva = y[..., :nq], y[..., nq:]
+    else:
+        q, kva = ops.linear(x, W.q), ops.linear(x, W.kva)
+    q = q.view(b, s, h, nope + r).transpose(1, 2)                      # [b,h,s,192] view
     latent = ops.rms_norm(kva[..., :lora], W.kva_norm, eps)            # strided rows, no copy
     kv = ops.kv_upproj(latent, W.kvb).view(b, s, h, nope + vd).transpose(1, 2)
     k_pe = kva[..., lora:].view(b, s, 1, r).transpose(1, 2)           # [b,1,s,64] view

@@ -47,3 +47,21 @@ def test_fragment_lane_order(dsk):
     for lane in range(64):
         np.testing.assert_array_equal(
             frag[lane], w[0, lane % 32, 8 * (lane // 32):8 * (lane // 32) + 8].numpy())
+
+
+@pytest.mark.parametrize("tiled", [True, False])
+def test_mla_merged_projection_weight_views(dsk, tiled):
+    """MLAWeights keeps q_proj and kv_a_proj in one [q rows; kva rows] matrix for
+    the single prefill GEMM; its q and kva fields are leading-dim slices of it and
+    equal the separately packed weights (tiled: 32-row blocks stay in order)."""
+    from ds_kernels import mla as dm
+    g = torch.Generator().manual_seed(4)
+    w = {"q": torch.randn(3072, 256, generator=g), "kva": torch.randn(576, 256, generator=g),
+         "kva_norm": torch.ones(512), "kvb": torch.randn(4096, 512, generator=g),
+         "o": torch.randn(256, 2048, generator=g)}
+    W = dm.MLAWeights.from_tensors(w, torch.device("cpu"), tiled=tiled)
+    pack = (lambda t: dsk.tile_weights(t.to(torch.bfloat16)[None])[0]) if tiled else \
+        (lambda t: t.to(torch.bfloat16))
+    assert torch.equal(W.q, pack(w["q"])) and torch.equal(W.kva, pack(w["kva"]))
+    assert W.q.data_ptr() == W.q_kva.data_ptr()
+    assert W.q.is_contiguous() and W.kva.is_contiguous()
