@@ -26,6 +26,9 @@ struct GemmArgs {
   int64_t c_group_stride;  // groups, and of the C bases (0: one base, rows by offsets)
   int b_tiled;             // B stored as MFMA fragments (see the fragment-tiled layout in
                            // dsk.h); ldb is then unused
+  uint16_t* C2;            // skinny kernel, optional: output columns n >= n_split go to
+  int64_t ldc2;            // C2[m * ldc2 + n - n_split] instead of C (n_split % 64 == 0)
+  int n_split;
 };
 
 int run_gemm(const GemmArgs& a, bool swiglu, hipStream_t st);

@@ -1176,10 +1176,13 @@ __global__ __launch_bounds__(kSkinnyThreads) void skinny_gemm_kernel(GemmArgs p,
         for (int c = 0; c < 4; ++c) v[c] += acc_read(acc[blk][mt][4 * qg + c]);
         return v;
       };
+      // a workgroup's 64 columns lie on one side of the split (n_split % 64 == 0)
+      const bool second = !SWIGLU && p.C2 != nullptr && nb * 64 >= p.n_split;
+      const int col0 = second ? p.n_split : 0;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const int m = m0 + mt * 32 + r32;
-        uint16_t* crow = Cg + (int64_t)m * p.ldc;
+        uint16_t* crow = second ? p.C2 + (int64_t)m * p.ldc2 : Cg + (int64_t)m * p.ldc;
         constexpr int JN = SWIGLU ? 1 : NB;
 #pragma unroll
         for (int j = 0; j < JN; ++j) {
@@ -1202,11 +1205,11 @@ __global__ __launch_bounds__(kSkinnyThreads) void skinny_gemm_kernel(GemmArgs p,
                 u32x2_t o;
                 o[0] = pack_bf16x2(v[0], v[1]);
                 o[1] = pack_bf16x2(v[2], v[3]);
-                *reinterpret_cast<u32x2_t*>(crow + n) = o;
+                *reinterpret_cast<u32x2_t*>(crow + (n - col0)) = o;
               } else {
 #pragma unroll
                 for (int c = 0; c < 4; ++c)
-                  if (n + c < p.N) crow[n + c] = f32_to_bf16(v[c]);
+                  if (n + c < p.N) crow[n - col0 + c] = f32_to_bf16(v[c]);
               }
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -1508,6 +1511,39 @@ extern "C" int dsk_linear_ex(const dsk_bf16* x, int64_t ld_x, const dsk_bf16* w,
   if (rc) return rc;
   DSK_REQUIRE(ld_out >= N, DSK_ERR_INVALID_ARG, "linear: ld_out < N");
   return run_gemm(a, false, as_stream(stream));
+}
+
+extern "C" int dsk_linear_split(const dsk_bf16* x, int64_t ld_x, const dsk_bf16* w_tiled,
+                                dsk_bf16* out0, int64_t ld_out0, dsk_bf16* out1,
+                                int64_t ld_out1, int M, int K, int N, int n_split,
+                                void* stream) {
+  DSK_REQUIRE(M >= 0, DSK_ERR_INVALID_ARG, "linear_split: M < 0");
+  DSK_REQUIRE(n_split > 0 && n_split < N && n_split % 64 == 0, DSK_ERR_INVALID_ARG,
+              "linear_split: n_split must be a multiple of 64 in (0, N)");
+  DSK_REQUIRE(ld_out0 >= n_split && ld_out1 >= N - n_split, DSK_ERR_INVALID_ARG,
+              "linear_split: ld_out0 < n_split or ld_out1 < N - n_split");
+  DSK_REQUIRE(out1 != nullptr, DSK_ERR_NULL_PTR, "linear_split: NULL pointer");
+  DSK_REQUIRE((reinterpret_cast<uintptr_t>(out1) & 7u) == 0 && ld_out1 % 4 == 0,
+              DSK_ERR_ALIGNMENT, "linear_split: out1 rows must be 8-byte aligned");
+  if (M == 0) return DSK_OK;
+  GemmArgs a{};
+  a.A = x; a.lda = ld_x;
+  a.B = w_tiled; a.ldb = K; a.b_group_stride = 0;
+  a.C = out0; a.ldc = ld_out0;
+  a.offsets = nullptr; a.G = 1;
+  a.M = M; a.N = N; a.K = K;
+  a.b_tiled = 1;
+  int rc = validate_gemm(a, "linear_split");
+  if (rc) return rc;
+  if (M <= kSkinnyMaxRows) {  // one launch, the destination chosen per workgroup
+    a.C2 = out1; a.ldc2 = ld_out1; a.n_split = n_split;
+    return run_gemm(a, false, as_stream(stream));
+  }
+  // larger M: two launches over the two row-block ranges of the tiled weight
+  rc = dsk_linear_ex(x, ld_x, w_tiled, DSK_LAYOUT_TILED, out0, ld_out0, M, K, n_split, stream);
+  if (rc) return rc;
+  const dsk_bf16* w1 = w_tiled + (int64_t)(n_split / 32) * (K / 16) * 512;
+  return dsk_linear_ex(x, ld_x, w1, DSK_LAYOUT_TILED, out1, ld_out1, M, K, N - n_split, stream);
 }
 
 extern "C" int dsk_linear_batched(const dsk_bf16* x, int64_t ld_x, int64_t x_batch_stride,

@@ -42,6 +42,7 @@ SIGNATURES = {
     "dsk_linear_ex": (_I, [_P, _I64, _P, _I, _P, _I64, _I, _I, _I, _P]),
     "dsk_attn_softmax": (_I, [_P, _I64, _I64, _I, _I, _F, _I, _P]),
     "dsk_linear_batched": (_I, [_P, _I64, _I64, _P, _P, _I64, _I64, _I, _I, _I, _I, _P]),
+    "dsk_linear_split": (_I, [_P, _I64, _P, _P, _I64, _P, _I64, _I, _I, _I, _I, _P]),
     "dsk_mla_decode_workspace_size": (_SZ, [_I, _I, _I]),
     "dsk_mla_decode_attention": (_I, [_P, _I64, _I64, _P, _I64, _I64, _P, _P, _I64, _I64, _P,
                                       _P, _F, _F, _I, _I, _I, _P, _I64, _I64, _P, _SZ, _P]),

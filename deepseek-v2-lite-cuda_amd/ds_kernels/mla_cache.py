@@ -207,13 +207,20 @@ def mla_decode_forward(x: torch.Tensor, W: MLAWeights, cache: LatentKVCache, cos
     A = absorbed if absorbed is not None else AbsorbedMLAWeights.from_mla(W)
     h, nope, r, vd, lora = W.n_heads, W.nope, W.rope_dim, W.v_dim, W.kv_lora
     T = b * n
-    q = ops.linear(x, W.q).view(T, h, nope + r)           # [T, h, 192]
     x2 = x.reshape(T, H)
     rows = cache.append_slots(n)                           # [b, n, 576] slots
-    if b == 1 or n == 1:                                   # one row stride: project in place
-        ops.linear(x2, W.kva, out=rows[0] if b == 1 else rows[:, 0])
+    nq = h * (nope + r)
+    if (b == 1 or n == 1) and W.q_kva is not None and W.q_kva.dim() == 4 and T <= 64:
+        # q_proj and kv_a_proj in one launch, kv_a's rows straight into the slots
+        q = torch.empty((T, nq), dtype=torch.bfloat16, device=x.device)
+        ops.linear_split(x2, W.q_kva, q, rows[0] if b == 1 else rows[:, 0])
+        q = q.view(T, h, nope + r)                         # [T, h, 192]
     else:
-        rows.copy_(ops.linear(x2, W.kva).view(b, n, lora + r))
+        q = ops.linear(x, W.q).view(T, h, nope + r)
+        if b == 1 or n == 1:                               # one row stride: project in place
+            ops.linear(x2, W.kva, out=rows[0] if b == 1 else rows[:, 0])
+        else:
+            rows.copy_(ops.linear(x2, W.kva).view(b, n, lora + r))
     L = cache.current_len
     if n >= UP_PROJECTED_MIN_TOKENS and L % 8 == 0 and L <= 4096:
         o = _attend_up_projected(q.view(b, n, h, nope + r), cache, W, cos, sin, eps)

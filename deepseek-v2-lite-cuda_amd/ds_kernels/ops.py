@@ -317,6 +317,33 @@ def linear(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor = None) -> t
     return out if given else out.view(*x.shape[:-1], N)
 
 
+def linear_split(x: torch.Tensor, weight: torch.Tensor, out0: torch.Tensor,
+                 out1: torch.Tensor) -> None:
+    """x[M, K] @ weight^T with columns [0, n0) written to out0 [M, n0] and the
+    rest to out1 [M, N - n0] (dsk_linear_split): one launch for M <= 64. weight
+    is fragment-tiled [N/32, K/16, 64, 8]; n0 = out0.shape[1] must be a multiple
+    of 64. Both outputs may be row-strided views with a contiguous last dim (for
+    example out1 = rows of a cache)."""
+    op = "linear_split"
+    _req(x.is_cuda and x.dtype == torch.bfloat16 and x.dim() == 2 and x.stride(1) == 1,
+         f"{op}: x must be a bf16 CUDA tensor [M, K] with a contiguous last dim.")
+    M, K = x.shape
+    _req(weight.is_cuda and weight.is_contiguous() and weight.dtype == torch.bfloat16 and
+         weight.dim() == 4 and tuple(weight.shape[2:]) == (64, 8) and weight.shape[1] * 16 == K,
+         f"{op}: weight must be tiled [N/32, {K // 16}, 64, 8].")
+    N = weight.shape[0] * 32
+    for name, o in (("out0", out0), ("out1", out1)):
+        _req(o.is_cuda and o.dtype == torch.bfloat16 and o.dim() == 2 and o.shape[0] == M and
+             o.stride(1) == 1, f"{op}: {name} must be bf16 [{M}, n] with a contiguous last dim.")
+    n0 = out0.shape[1]
+    _req(n0 + out1.shape[1] == N, f"{op}: out0 and out1 widths must add up to {N}.")
+    if M:
+        with torch.cuda.device(x.device):
+            check(lib.dsk_linear_split(x.data_ptr(), x.stride(0), weight.data_ptr(),
+                                       out0.data_ptr(), out0.stride(0), out1.data_ptr(),
+                                       out1.stride(0), M, K, N, n0, stream_handle(x.device)), op)
+
+
 def linear_batched(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor = None) -> torch.Tensor:
     """out[b] = x[b] @ weight[b]^T for every entry b of a batch, in one launch
     (dsk_linear_batched), up to 64 rows per entry. x: bf16 [batch, M, K], any

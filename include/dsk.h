@@ -212,6 +212,21 @@ int dsk_rope_qk(const dsk_bf16* q, int64_t qsb, int64_t qsh, int64_t qss,
                 int64_t cs, dsk_bf16* q_out, dsk_bf16* k_out, int B, int Hq,
                 int Hk, int S, int d, void* stream);
 
+/* ----------------------------------------------------- two-output linear --
+ * x[M, K] @ w^T with w fragment-tiled [N/32, K/16, 64, 8], output columns
+ * [0, n_split) to out0 (row pitch ld_out0) and [n_split, N) to out1 (row pitch
+ * ld_out1, column n at out1[m * ld_out1 + n - n_split]); n_split % 64 == 0.
+ * For M <= 64 this is one launch of the small-group kernel, which picks the
+ * destination per 64-column workgroup; larger M runs as two launches over the
+ * weight's two row-block ranges. Lets the absorbed-MLA decode step run q_proj
+ * and kv_a_proj (mla.py:318-334) as one launch with kv_a's rows written
+ * straight into the latent cache; the reference has no counterpart (it runs
+ * the two projections as separate torch GEMMs and copies into its cache,
+ * mla_cache.py:104-147). */
+int dsk_linear_split(const dsk_bf16* x, int64_t ld_x, const dsk_bf16* w_tiled,
+                     dsk_bf16* out0, int64_t ld_out0, dsk_bf16* out1, int64_t ld_out1,
+                     int M, int K, int N, int n_split, void* stream);
+
 /* --------------------------------------------------------- batched linear --
  * out[b] = x[b] @ w[b]^T for b < batch, with M <= 64 rows per entry (the
  * weight-streaming small-group kernel; one launch for all entries). Entry b of

@@ -69,6 +69,20 @@ def test_error_text_is_per_thread(dsk):
     assert rc0 == rc1 == 1 and "num_experts" in m0 and "top_k" in m1
 
 
+def test_linear_split_validation(dsk):
+    lib = dsk.lib
+    # argument order: x, ld_x, w, out0, ld_out0, out1, ld_out1, M, K, N, n_split, stream
+    def call(n_split=3072, ld0=3072, ld1=576, out1=16, M=1, N=3648):
+        return lib.dsk_linear_split(16, 2048, 16, 16, ld0, out1, ld1, M, 2048, N, n_split, None)
+    assert call(n_split=3000) == 1 and "multiple of 64" in _err(dsk)
+    assert call(n_split=3648) == 1 and "multiple of 64" in _err(dsk)
+    assert call(ld0=3000) == 1 and "ld_out0" in _err(dsk)
+    assert call(ld1=500) == 1 and "ld_out1" in _err(dsk)
+    assert call(out1=None) == 2
+    assert call(out1=20) == 3 and "8-byte" in _err(dsk)
+    assert call(M=0) == 0  # nothing to do, nothing launched
+
+
 def test_routing_limits_rejected(dsk):
     lib = dsk.lib
     rc = lib.dsk_moe_routing(None, 65, None, None, 8, 4, 65, 6, None, 0, None)

@@ -138,3 +138,23 @@ def test_linear_batched_strided_views(setup, M, K, N):
     ref = torch.einsum("hmk,hnk->hmn", big[..., :K].transpose(0, 1).float(), w.float())
     assert max_rel_err(np32(out), ref.numpy()) <= BF16_TOL
     assert torch.count_nonzero(out_full[..., N:]) == 0   # nothing written past the slice
+
+
+@pytest.mark.parametrize("M,n0", [(1, 3072), (16, 3072), (64, 64), (100, 3072)])
+def test_linear_split_matches_linear(setup, M, n0):
+    """dsk_linear_split (one small-group launch for M <= 64, two launches over the
+    weight's row blocks above) equals the one-output projection bit for bit; out1
+    is a strided view (rows of a wider buffer), and nothing lands past its columns."""
+    dsk = setup[0]
+    g = torch.Generator().manual_seed(M + n0)
+    x = torch.randn(M, 2048, generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(3648, 2048, generator=g) * 0.02).to(torch.bfloat16)
+    wt = dsk.tile_weights(w[None])[0].to(DEV)
+    full = dsk.linear(x, wt)
+    out0 = torch.empty(M, n0, dtype=torch.bfloat16, device=DEV)
+    pad = torch.zeros(M, 3648 - n0 + 64, dtype=torch.bfloat16, device=DEV)
+    dsk.linear_split(x, wt, out0, pad[:, :3648 - n0])
+    torch.cuda.synchronize()
+    assert torch.equal(out0, full[:, :n0])
+    assert torch.equal(pad[:, :3648 - n0], full[:, n0:])
+    assert torch.count_nonzero(pad[:, 3648 - n0:]) == 0
