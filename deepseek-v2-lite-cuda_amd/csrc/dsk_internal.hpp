@@ -46,6 +46,12 @@ int launch_gate_parts(const uint16_t* x, int64_t ld_x, const uint16_t* wg, bool 
                       float* parts, int T, int E, int H, int n_parts, hipStream_t st);
 int launch_scan(const int32_t* hist, int nblk, int E, int32_t* counts, int32_t* offsets,
                 int32_t* blk_base, int n_extra_groups, int extra_rows, hipStream_t st);
+// Scan + permutation in one launch (the fused layer's T > 64 path): offsets,
+// counts, token_map and slot_of from the chunk histograms and in-chunk ranks.
+int launch_scan_permute(const int32_t* hist, int nblk, const int32_t* idx, int T, int K,
+                        int E, const int32_t* local_rank, int S, int32_t* counts,
+                        int32_t* offsets, int32_t* token_map, int32_t* slot_of,
+                        int n_extra_groups, hipStream_t st);
 int launch_permute(const int32_t* idx, const float* w, int T, int K, int E,
                    const int32_t* offsets, const int32_t* blk_base, const int32_t* local_rank,
                    int S, int32_t* token_map, float* dw, int32_t* slot_of, int n_extra_groups,

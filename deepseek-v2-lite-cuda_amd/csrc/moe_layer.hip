@@ -1,8 +1,8 @@
 // Fused DeepSeekMoE forward on one GPU: the whole layer (moe.py:77-109) as one
-// C call that enqueues 4-7 kernels on the caller's stream and never waits.
+// C call that enqueues 4-6 kernels on the caller's stream and never waits.
 //
 //   [partial gate sums, dsk_moe_layer_forward only]  ->
-//   route (+histogram, ranks)  ->  [scan + permute when T > 64]  ->
+//   route (+histogram, ranks)  ->  [scan + permute, one kernel, when T > 64]  ->
 //   grouped GEMM1 + SwiGLU (A rows gathered from x through token_map)  ->
 //   grouped GEMM2  ->  combine (ascending-expert fp32 sum + shared rows, one
 //   bf16 rounding)
@@ -19,7 +19,7 @@
 namespace dsk {
 
 struct FusedLayout {
-  size_t hist, base, rank, idx, w, counts, offsets, token_map, slot_of, h, y, total;
+  size_t hist, rank, idx, w, counts, offsets, token_map, slot_of, h, y, total;
 };
 
 static FusedLayout fused_layout(int T, int E, int K, int nsh, int H, int I) {
@@ -34,7 +34,6 @@ static FusedLayout fused_layout(int T, int E, int K, int nsh, int H, int I) {
     return o;
   };
   L.hist = take((size_t)nblk * E * 4);
-  L.base = take((size_t)nblk * E * 4);
   L.rank = take(S * 4);
   L.idx = take(S * 4);
   L.w = take(S * 4);
@@ -58,7 +57,6 @@ static int layer_after_gate(const float* logits, int n_parts, int64_t part_strid
                             float* topk_w_out, int32_t* expert_offsets_out, char* ws,
                             const FusedLayout& L, void* const* stage_events, hipStream_t st) {
   int32_t* hist = reinterpret_cast<int32_t*>(ws + L.hist);
-  int32_t* base = reinterpret_cast<int32_t*>(ws + L.base);
   int32_t* rank = reinterpret_cast<int32_t*>(ws + L.rank);
   int32_t* idx = topk_idx_out ? topk_idx_out : reinterpret_cast<int32_t*>(ws + L.idx);
   float* w = topk_w_out ? topk_w_out : reinterpret_cast<float*>(ws + L.w);
@@ -89,10 +87,8 @@ static int layer_after_gate(const float* logits, int n_parts, int64_t part_strid
     rc = launch_route(logits, E, n_parts, part_stride, bias, T, E, K, idx, w, hist, rank,
                       nullptr, nullptr, nullptr, nullptr, 0, st);
     if (rc) return rc;
-    rc = launch_scan(hist, nblk, E, counts, offsets, base, nsh, T, st);
-    if (rc) return rc;
-    rc = launch_permute(idx, w, T, K, E, offsets, base, rank, S, token_map, nullptr, slot_of,
-                        nsh, st);
+    rc = launch_scan_permute(hist, nblk, idx, T, K, E, rank, S, counts, offsets, token_map,
+                             slot_of, nsh, st);
     if (rc) return rc;
   }
 

@@ -273,6 +273,94 @@ __global__ __launch_bounds__(256) void permute_kernel(
   }
 }
 
+// ---------------------------------------------------------- scan+permute ----
+// The scan and the permutation in one launch, for the fused layer. Workgroup
+// b < ceil(T / 32) owns the (token, k) pairs of tokens 32b .. 32b+31, which lie
+// in one 64-token chunk; it reduces the chunk histograms itself (nblk x E
+// ints, 16 KB at T = 4096, read from L2) into the expert offsets and its
+// chunk's bases, then assigns the slots as permute_kernel does. The sums are
+// integer, so every workgroup sees the same offsets; workgroup 0 also writes
+// counts and offsets. The workgroups after those write the identity rows of
+// the always-on groups.
+constexpr int kScanPermThreads = 256;
+constexpr int kScanPermSegs = kScanPermThreads / 64;
+constexpr int kScanPermTokens = 32;  // tokens per workgroup: K <= 8 pairs each
+
+__global__ __launch_bounds__(kScanPermThreads) void scan_permute_kernel(
+    const int32_t* __restrict__ hist, int nblk, const int32_t* __restrict__ idx, int T, int K,
+    int E, const int32_t* __restrict__ local_rank, int S, int32_t* __restrict__ counts,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ token_map,
+    int32_t* __restrict__ slot_of, int n_extra_groups) {
+  __shared__ int s_all[kScanPermSegs][64];
+  __shared__ int s_lo[kScanPermSegs][64];
+  __shared__ int s_off[64];
+  __shared__ int s_base[64];
+  const int tid = threadIdx.x, e = tid & 63, sg = tid >> 6;
+  const int n_pair_wgs = (T + kScanPermTokens - 1) / kScanPermTokens;
+  if ((int)blockIdx.x >= n_pair_wgs) {  // uniform: rows of the always-on groups
+    const int64_t q = (int64_t)(blockIdx.x - n_pair_wgs) * kScanPermThreads + tid;
+    if (q < (int64_t)n_extra_groups * T) token_map[S + q] = (int)(q % T);
+    return;
+  }
+  const int t0 = blockIdx.x * kScanPermTokens;
+  const int chunk = t0 / kChunk;
+  // segment sums of every chunk's histogram, and of the chunks below this one
+  const int seg = (nblk + kScanPermSegs - 1) / kScanPermSegs;
+  const int b0 = min(sg * seg, nblk), b1 = min(b0 + seg, nblk);
+  int all = 0, lo = 0;
+  if (e < E) {
+    // batches of 8 independent loads, so a batch costs one round trip
+    for (int b = b0; b < b1; b += 8) {
+      int v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = b + u < b1 ? hist[(int64_t)(b + u) * E + e] : 0;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        all += v[u];
+        lo += b + u < chunk ? v[u] : 0;
+      }
+    }
+  }
+  s_all[sg][e] = all;
+  s_lo[sg][e] = lo;
+  __syncthreads();
+  if (sg == 0) {
+    int tot = 0, below = 0;
+#pragma unroll
+    for (int k = 0; k < kScanPermSegs; ++k) {
+      tot += s_all[k][e];
+      below += s_lo[k][e];
+    }
+    const int inc = wave_inclusive_scan(tot);  // lanes e >= E hold 0
+    s_off[e] = inc - tot;
+    s_base[e] = below;
+    if (blockIdx.x == 0) {
+      if (e < E) {
+        if (counts != nullptr) counts[e] = tot;
+        offsets[e] = inc - tot;
+      }
+      if (e == 63) {
+        offsets[E] = inc;
+        for (int j = 1; j <= n_extra_groups; ++j) offsets[E + j] = inc + j * T;
+      }
+    }
+  }
+  __syncthreads();
+  const int64_t npairs = (int64_t)T * K;
+  const int64_t p = (int64_t)t0 * K + tid;
+  if (tid < kScanPermTokens * K && p < npairs) {
+    const int ex = idx[p];
+    const int r = local_rank[p];
+    int slot = -1;
+    if (ex >= 0 && ex < E && r >= 0) {
+      slot = s_off[ex] + s_base[ex] + r;
+      if (slot < 0 || slot >= S) slot = -1;
+    }
+    if (slot >= 0) token_map[slot] = (int)(p / K);
+    if (slot_of != nullptr) slot_of[p] = slot;
+  }
+}
+
 // -------------------------------------------------------------- dispatch ----
 // Row gather dispatched[slot] = x[t]: one wave per (token, k) pair, 16 B/lane.
 __global__ __launch_bounds__(256) void gather_rows_kernel(
@@ -511,6 +599,21 @@ int launch_scan(const int32_t* hist, int nblk, int E, int32_t* counts, int32_t* 
   hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(kScanThreads), 0, st, hist, nblk, E,
                      counts, offsets, blk_base, n_extra_groups, extra_rows);
   return check_launch("scan_kernel");
+}
+
+int launch_scan_permute(const int32_t* hist, int nblk, const int32_t* idx, int T, int K,
+                        int E, const int32_t* local_rank, int S, int32_t* counts,
+                        int32_t* offsets, int32_t* token_map, int32_t* slot_of,
+                        int n_extra_groups, hipStream_t st) {
+  if (T == 0) return DSK_OK;
+  if (K > kScanPermThreads / kScanPermTokens || E > 64)
+    return fail(DSK_ERR_INVALID_ARG, "scan_permute: needs top_k <= 8 and at most 64 experts");
+  const int64_t n_wgs = (T + kScanPermTokens - 1) / kScanPermTokens +
+                        ((int64_t)n_extra_groups * T + kScanPermThreads - 1) / kScanPermThreads;
+  hipLaunchKernelGGL(scan_permute_kernel, dim3((unsigned)n_wgs), dim3(kScanPermThreads), 0, st,
+                     hist, nblk, idx, T, K, E, local_rank, S, counts, offsets, token_map,
+                     slot_of, n_extra_groups);
+  return check_launch("scan_permute_kernel");
 }
 
 int launch_permute(const int32_t* idx, const float* w, int T, int K, int E,
