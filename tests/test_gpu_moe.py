@@ -434,3 +434,38 @@ def test_concurrent_calls_on_two_streams(dsk, full_layer, tiled_layer):
     for i in range(2):
         for r in range(4):
             assert torch.equal(results[i][r], ref[i]), (i, r)
+
+
+@pytest.mark.parametrize("T,E,K,nsh", [(65, 8, 1, 0), (100, 16, 2, 2), (300, 64, 6, 2),
+                                       (1000, 8, 1, 2), (777, 64, 3, 0), (4097, 16, 6, 2)])
+def test_fused_layer_small_shapes_routing_and_output(dsk, T, E, K, nsh):
+    """The T > 64 routing of the fused layer (route, then the scan and the
+    permutation in one kernel, 32 tokens per workgroup) for other expert counts,
+    top-k values, token counts that are not multiples of 32 or 64, and with or
+    without shared groups: offsets and indices bit-exact against the oracle,
+    the layer output within the bf16 bar."""
+    H, I = 256, 128
+    g = torch.Generator().manual_seed(T * 7 + E + K)
+    gates = (torch.randn(E, I, H, generator=g) * 0.05).to(torch.bfloat16)
+    ups = (torch.randn(E, I, H, generator=g) * 0.05).to(torch.bfloat16)
+    downs = (torch.randn(E, H, I, generator=g) * 0.05).to(torch.bfloat16)
+    shared = None
+    if nsh:
+        shared = tuple((torch.randn(*s, generator=g) * 0.05).to(torch.bfloat16)
+                       for s in ((nsh * I, H), (nsh * I, H), (H, nsh * I)))
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    logits = torch.randn(T, E, generator=g)
+    w1, w2, n = dsk.pack_tensors(gates, ups, downs, device=torch.device(DEV), shared=shared)
+    assert n == nsh
+    out, (idx, w, off) = dsk.moe_fused_forward_logits(logits.to(DEV), x.to(DEV), w1, w2, K, n,
+                                                      E, return_routing=True)
+    torch.cuda.synchronize()
+    lg = logits.numpy()
+    ridx, rw, rcounts = om.route(lg, K)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+    roff = om.scan(rcounts)
+    np.testing.assert_array_equal(off.cpu().numpy()[:E + 1], roff)
+    f = lambda t: t.float().numpy()  # noqa: E731
+    ref = om.moe_layer(f(x), None, f(gates), f(ups), f(downs), K,
+                       shared=tuple(f(t) for t in shared) if shared else None, logits=lg)
+    assert max_rel_err(np32(out), ref) <= BF16_TOL
