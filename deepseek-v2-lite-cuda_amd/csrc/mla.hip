@@ -299,13 +299,16 @@ __global__ __launch_bounds__(256) void attn_softmax_kernel(uint16_t* __restrict_
       sum += v[c][e];
     }
   sum = wave_sum(sum);
+  // one division per row, then products: within an fp32 ulp of p / sum, far
+  // below the bf16 rounding of the result, and a fraction of the ALU work
+  const float inv = 1.f / sum;
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const int col = c * 512 + lane * 8;
     if (col < kv_len) {
       u32x4_t o;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = pack_bf16x2(v[c][2 * e] / sum, v[c][2 * e + 1] / sum);
+      for (int e = 0; e < 4; ++e) o[e] = pack_bf16x2(v[c][2 * e] * inv, v[c][2 * e + 1] * inv);
       *reinterpret_cast<u32x4_t*>(p + col) = o;
     }
   }
