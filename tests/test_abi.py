@@ -244,3 +244,35 @@ def test_python_ops_reject_cpu_tensors(dsk):
         dsk.moe_scan(torch.zeros(64, dtype=torch.int32))
     with pytest.raises(RuntimeError):
         dsk.rms_norm(torch.zeros(2, 8, dtype=torch.bfloat16), torch.ones(8))
+
+
+def test_c_caller_links_and_calls(dsk, tmp_path):
+    """A plain C99 caller (what a cgo / JNI / N-API stub compiles against):
+    include/dsk.h compiles as C, links against libdsk.so, and the entry points
+    answer without a GPU (version, a rejected argument and its message)."""
+    import shutil
+    import subprocess
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    src = tmp_path / "caller.c"
+    src.write_text(r"""
+#include <stdio.h>
+#include <string.h>
+#include "dsk.h"
+int main(void) {
+  if (dsk_abi_version() != 2) return 1;
+  /* top_k = 7 is rejected before any device work */
+  int rc = dsk_moe_routing(NULL, 64, NULL, NULL, NULL, 4, 64, 7, NULL, 0, NULL);
+  if (rc != 1 || strstr(dsk_last_error(), "top_k") == NULL) return 2;
+  printf("ok\n");
+  return 0;
+}
+""")
+    exe = tmp_path / "caller"
+    libdir = os.path.dirname(dsk.LIB_PATH)
+    subprocess.run([cc, "-std=c99", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"),
+                    str(src), "-o", str(exe), os.path.join(libdir, "libdsk.so"),
+                    "-Wl,-rpath," + libdir], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 0 and out.stdout.strip() == "ok", (out.returncode, out.stderr)
