@@ -145,9 +145,13 @@ def mla_forward(x: torch.Tensor, W: MLAWeights, cos: torch.Tensor, sin: torch.Te
     x: bf16 [b, s, H] -> bf16 [b, s, H]."""
     b, s, H = x.shape
     q_nope, q_rot, k_nope, v, k_rot, _ = mla_projections(x, W, cos, sin, eps)
+    h, nope, r = W.n_heads, W.nope, W.rope_dim
     q = torch.cat([q_nope, q_rot], dim=-1)                             # [b,h,s,192]
-    k = torch.cat([k_nope, k_rot.expand(b, W.n_heads, s, W.rope_dim)], dim=-1)
-    scores = torch.matmul(q, k.transpose(-1, -2).contiguous())        # bf16 [b,h,s,s]
+    # K^T built in place, contiguous (one pass instead of a cat and a transposed copy)
+    kT = torch.empty((b, h, nope + r, s), dtype=torch.bfloat16, device=x.device)
+    kT[:, :, :nope].copy_(k_nope.transpose(-1, -2))
+    kT[:, :, nope:].copy_(k_rot.transpose(-1, -2).expand(b, h, r, s))
+    scores = torch.matmul(q, kT)                                       # bf16 [b,h,s,s]
     p = ops.attn_softmax_(scores, W.softmax_scale, causal=True)       # scale, mask, softmax
     o = torch.matmul(p, v.contiguous())                                # [b,h,s,v]
     o = o.transpose(1, 2).reshape(b, s, W.n_heads * W.v_dim)
