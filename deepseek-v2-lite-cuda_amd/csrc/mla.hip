@@ -194,54 +194,103 @@ struct RopeTensor {
   int heads;
 };
 
-// One thread per 8 elements (4 pairs) with 32-bit index arithmetic (a 64-bit
-// division per element would cost more than the memory traffic).
+// Division by a divisor fixed for the launch, for indices below 2^31, as a
+// high multiply and a shift (Granlund and Montgomery, "Division by invariant
+// integers using multiplication", 1994): with l = ceil(log2 d),
+// m = ceil(2^(31+l) / d), q = umulhi(x, m) >> (l - 1); d = 1 is m = 0.
+struct FastDiv {
+  uint32_t m, s;
+  int d;
+};
+static FastDiv make_fastdiv(int d) {
+  FastDiv f{0u, 0u, d};
+  if (d <= 1) return f;
+  uint32_t l = 0;
+  while ((1ull << l) < (uint64_t)d) ++l;
+  f.m = (uint32_t)(((1ull << (31 + l)) + (uint64_t)d - 1) / (uint64_t)d);
+  f.s = l - 1;
+  return f;
+}
+__device__ __forceinline__ int fdiv(int x, const FastDiv& f) {
+  return f.m == 0 ? x : (int)(__umulhi((uint32_t)x, f.m) >> f.s);
+}
+
+// NP consecutive bf16 values (NP = 4: 8 bytes, NP = 8: 16 bytes) as packed pairs
+template <int NP>
+__device__ __forceinline__ void load_bf16(const uint16_t* p, uint32_t (&v)[NP / 2]) {
+  if constexpr (NP == 8) {
+    const u32x4_t w = *reinterpret_cast<const u32x4_t*>(p);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = w[k];
+  } else {
+    const u32x2_t w = *reinterpret_cast<const u32x2_t*>(p);
+    v[0] = w[0];
+    v[1] = w[1];
+  }
+}
+template <int NP>
+__device__ __forceinline__ void store_bf16(uint16_t* p, const uint32_t (&v)[NP / 2]) {
+  if constexpr (NP == 8) {
+    *reinterpret_cast<u32x4_t*>(p) = u32x4_t{v[0], v[1], v[2], v[3]};
+  } else {
+    *reinterpret_cast<u32x2_t*>(p) = u32x2_t{v[0], v[1]};
+  }
+}
+
+// One thread per NP pairs (2 * NP elements; NP = 8 when the rope dim is a
+// multiple of 16, else 4), with 32-bit index arithmetic and the row index
+// split by multiply-shift division (the divisors are fixed per launch).
+template <int NP>
 __global__ __launch_bounds__(256) void rope_kernel(RopeTensor a, RopeTensor b, int items_a,
                                                    int items_b,
                                                    const uint16_t* __restrict__ cos_t,
                                                    const uint16_t* __restrict__ sin_t,
-                                                   int64_t cb, int64_t cs, int S, int d) {
+                                                   int64_t cb, int64_t cs, int d, FastDiv div_cpr,
+                                                   FastDiv div_s, FastDiv div_ha,
+                                                   FastDiv div_hb) {
   int i = blockIdx.x * 256 + threadIdx.x;
   if (i >= items_a + items_b) return;
   const bool is_a = i < items_a;
   const RopeTensor& r = is_a ? a : b;
   if (!is_a) i -= items_a;
-  const int cpr = d >> 3;
   const int half = d >> 1;
-  const int row = i / cpr;               // output row = (bb * heads + h) * S + s
-  const int c = i - row * cpr;
-  const int bh = row / S;
-  const int s = row - bh * S;
-  const int bb = bh / r.heads;
+  const int row = fdiv(i, div_cpr);      // output row = (bb * heads + h) * S + s
+  const int c = i - row * div_cpr.d;
+  const int bh = fdiv(row, div_s);
+  const int s = row - bh * div_s.d;
+  const int bb = fdiv(bh, is_a ? div_ha : div_hb);
   const int h = bh - bb * r.heads;
-  const uint16_t* xp = r.x + bb * r.sb + h * r.sh + (int64_t)s * r.ss + c * 8;
+  const uint16_t* xp = r.x + bb * r.sb + h * r.sh + (int64_t)s * r.ss + c * 2 * NP;
   const int64_t toff = bb * cb + (int64_t)s * cs;
-  const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(xp);
-  const u32x2_t clo = *reinterpret_cast<const u32x2_t*>(cos_t + toff + 4 * c);
-  const u32x2_t chi = *reinterpret_cast<const u32x2_t*>(cos_t + toff + half + 4 * c);
-  const u32x2_t slo = *reinterpret_cast<const u32x2_t*>(sin_t + toff + 4 * c);
-  const u32x2_t shi = *reinterpret_cast<const u32x2_t*>(sin_t + toff + half + 4 * c);
-  float lo[4], hi[4];
+  uint32_t xv[NP], cl[NP / 2], ch[NP / 2], sl[NP / 2], sh[NP / 2];
+  load_bf16<NP>(xp, *reinterpret_cast<uint32_t(*)[NP / 2]>(&xv[0]));
+  load_bf16<NP>(xp + NP, *reinterpret_cast<uint32_t(*)[NP / 2]>(&xv[NP / 2]));
+  load_bf16<NP>(cos_t + toff + NP * c, cl);
+  load_bf16<NP>(cos_t + toff + half + NP * c, ch);
+  load_bf16<NP>(sin_t + toff + NP * c, sl);
+  load_bf16<NP>(sin_t + toff + half + NP * c, sh);
+  uint32_t olo[NP / 2], ohi[NP / 2];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float x0 = bf16lo(xv[j]);  // x[2k]
-    const float x1 = bf16hi(xv[j]);  // x[2k+1]
-    const uint32_t cl = clo[j >> 1], ch = chi[j >> 1], sl = slo[j >> 1], sh = shi[j >> 1];
-    const float c_lo = (j & 1) ? bf16hi(cl) : bf16lo(cl);
-    const float c_hi = (j & 1) ? bf16hi(ch) : bf16lo(ch);
-    const float s_lo = (j & 1) ? bf16hi(sl) : bf16lo(sl);
-    const float s_hi = (j & 1) ? bf16hi(sh) : bf16lo(sh);
-    lo[j] = x0 * c_lo - x1 * s_lo;
-    hi[j] = x1 * c_hi + x0 * s_hi;
+  for (int j = 0; j < NP; j += 2) {
+    float lo[2], hi[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int k = j + u;
+      const float x0 = bf16lo(xv[k]);  // x[2k]
+      const float x1 = bf16hi(xv[k]);  // x[2k+1]
+      const float c_lo = u ? bf16hi(cl[k >> 1]) : bf16lo(cl[k >> 1]);
+      const float c_hi = u ? bf16hi(ch[k >> 1]) : bf16lo(ch[k >> 1]);
+      const float s_lo = u ? bf16hi(sl[k >> 1]) : bf16lo(sl[k >> 1]);
+      const float s_hi = u ? bf16hi(sh[k >> 1]) : bf16lo(sh[k >> 1]);
+      lo[u] = x0 * c_lo - x1 * s_lo;
+      hi[u] = x1 * c_hi + x0 * s_hi;
+    }
+    olo[j >> 1] = pack_bf16x2(lo[0], lo[1]);
+    ohi[j >> 1] = pack_bf16x2(hi[0], hi[1]);
   }
   uint16_t* op = r.out + (int64_t)row * d;
-  u32x2_t olo, ohi;
-  olo[0] = pack_bf16x2(lo[0], lo[1]);
-  olo[1] = pack_bf16x2(lo[2], lo[3]);
-  ohi[0] = pack_bf16x2(hi[0], hi[1]);
-  ohi[1] = pack_bf16x2(hi[2], hi[3]);
-  *reinterpret_cast<u32x2_t*>(op + 4 * c) = olo;
-  *reinterpret_cast<u32x2_t*>(op + half + 4 * c) = ohi;
+  store_bf16<NP>(op + NP * c, olo);
+  store_bf16<NP>(op + half + NP * c, ohi);
 }
 
 static int check_rope(const void* x, int64_t sb, int64_t sh, int64_t ss, const void* out,
@@ -367,10 +416,18 @@ extern "C" int dsk_rope_qk(const dsk_bf16* q, int64_t qsb, int64_t qsh, int64_t 
               "rope: more than 2^31 8-element chunks");
   RopeTensor a{q, qsb, qsh, qss, q_out, Hq > 0 ? Hq : 1};
   RopeTensor b{k, ksb, ksh, kss, k_out, Hk > 0 ? Hk : 1};
-  const int items_q = (int)(rows_q * (d / 8)), items_k = (int)(rows_k * (d / 8));
+  const int np = d % 16 == 0 ? 8 : 4;  // pairs per thread
+  const int cpr = d / (2 * np);          // threads per row
+  const int items_q = (int)(rows_q * cpr), items_k = (int)(rows_k * cpr);
   const unsigned grid = (unsigned)(((int64_t)items_q + items_k + 255) / 256);
-  hipLaunchKernelGGL(rope_kernel, dim3(grid), dim3(256), 0, as_stream(stream), a, b, items_q,
-                     items_k, cos_t, sin_t, cb, cs, S, d);
+  const FastDiv dc = make_fastdiv(cpr), ds = make_fastdiv(S > 0 ? S : 1);
+  const FastDiv dha = make_fastdiv(a.heads), dhb = make_fastdiv(b.heads);
+  if (np == 8)
+    hipLaunchKernelGGL(rope_kernel<8>, dim3(grid), dim3(256), 0, as_stream(stream), a, b, items_q,
+                       items_k, cos_t, sin_t, cb, cs, d, dc, ds, dha, dhb);
+  else
+    hipLaunchKernelGGL(rope_kernel<4>, dim3(grid), dim3(256), 0, as_stream(stream), a, b, items_q,
+                       items_k, cos_t, sin_t, cb, cs, d, dc, ds, dha, dhb);
   return check_launch("rope_kernel");
 }
 
