@@ -82,6 +82,25 @@ def test_rope_matches_oracle(dsk, b, s, strided):
     np.testing.assert_allclose(np32(q_rot), rq, rtol=2 ** -7, atol=2e-3)
 
 
+@pytest.mark.parametrize("d,hq,s", [(8, 3, 37), (24, 3, 37), (32, 16, 5), (48, 2, 64),
+                                    (128, 5, 9)])
+def test_rope_other_dims(dsk, d, hq, s):
+    """Rope dims other than 64: 4 pairs per thread when d is not a multiple of 16
+    (8, 24), 8 pairs otherwise; odd head counts and sequence lengths exercise the
+    multiply-shift index split. The cos/sin tables are random, not duplicated
+    halves, so the first- and second-half table reads are told apart."""
+    b = 2
+    g = torch.Generator().manual_seed(d * 100 + hq + s)
+    q = torch.randn(b, hq, s, d, generator=g).to(torch.bfloat16)
+    k = torch.randn(b, 1, s, d, generator=g).to(torch.bfloat16)
+    cos = (torch.rand(b, 1, s, d, generator=g) * 2 - 1).to(torch.bfloat16)
+    sin = (torch.rand(b, 1, s, d, generator=g) * 2 - 1).to(torch.bfloat16)
+    q_rot, k_rot = dsk.rope(q.to(DEV), k.to(DEV), cos.to(DEV), sin.to(DEV))
+    c, sn = np32(cos), np32(sin)
+    np.testing.assert_allclose(np32(q_rot), ol.rope(np32(q), c, sn), rtol=2 ** -7, atol=2e-3)
+    np.testing.assert_allclose(np32(k_rot), ol.rope(np32(k), c, sn), rtol=2 ** -7, atol=2e-3)
+
+
 @pytest.mark.parametrize("rows", [1, 64, 4096])
 def test_kv_upproj(dsk, rows):
     g = torch.Generator().manual_seed(rows)
