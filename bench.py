@@ -19,7 +19,8 @@ Also reported on the same line:
                 strided latent, rope, kv_upproj, each timed by HIP-graph replay) and
                 the decoder layer, composed from this library's kernels.
   cpu_baseline  the CPU oracle (numpy restatement of DeepSeekMoE.forward) timed
-                on a bounded sample (config 0, T=64 fp32) on this host's cores.
+                on this host's cores: the same T=4096 workload (2 calls, fp32; the
+                reported value) and config 0 (T=64) beside it.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
                        [--profile | --decode-only T | --mla-only | --mla-decode-only]
@@ -300,7 +301,23 @@ def bench_latent_decode(dsk, torch, dm, W, timed, dev, g):
     return res
 
 
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
 def cpu_baseline(W, syn, budget_s):
+    """The CPU oracle (numpy fp32 restatement of DeepSeekMoE.forward, reference
+    src/reference/moe.py:77-109) on this host: the same workload as the GPU line
+    (T=4096, 2 timed calls after one warm-up) and config 0 (T=64, calls until
+    budget_s). `value` is the T=4096 rate."""
     import numpy as np
     from oracle import moe as om
     try:
@@ -309,21 +326,30 @@ def cpu_baseline(W, syn, budget_s):
                        if p.get("user_api") == "blas"] or [1])
     except Exception:  # pragma: no cover
         threads = os.cpu_count() or 1
-    T = 64
-    x = syn.tokens(T).numpy()
-    args = (x, W.wg.numpy(), W.gates.numpy(), W.ups.numpy(), W.downs.numpy(), 6)
+    wts = (W.wg.numpy(), W.gates.numpy(), W.ups.numpy(), W.downs.numpy())
     shared = tuple(t.numpy() for t in W.shared)
-    om.moe_layer(*args, shared=shared)          # warm-up
-    n, t0 = 0, time.perf_counter()
-    while True:
-        om.moe_layer(*args, shared=shared)
-        n += 1
-        el = time.perf_counter() - t0
-        if (el >= budget_s and n >= 2) or n >= 200:
-            break
-    return {"value": T * n / el, "unit": "tokens/s", "cores": int(threads), "kind": "port",
-            "sample": f"oracle DeepSeekMoE.forward restatement (numpy fp32), config 0: T=64, "
-                      f"{n} calls in {el:.1f} s, BLAS threads={threads}, host cpus={os.cpu_count()}"}
+
+    def rate(T, min_calls, max_calls, budget):
+        x = syn.tokens(T).numpy()
+        om.moe_layer(x, *wts, 6, shared=shared)          # warm-up
+        n, t0 = 0, time.perf_counter()
+        while True:
+            om.moe_layer(x, *wts, 6, shared=shared)
+            n += 1
+            el = time.perf_counter() - t0
+            if (el >= budget and n >= min_calls) or n >= max_calls:
+                return T * n / el, n, el
+
+    v4096, n4096, e4096 = rate(4096, 2, 2, 0.0)
+    v64, n64, e64 = rate(64, 2, 200, budget_s)
+    model = _cpu_model()
+    return {"value": v4096, "unit": "tokens/s", "cores": int(threads), "kind": "port",
+            "sample": f"oracle DeepSeekMoE.forward restatement (numpy fp32) on {model}: "
+                      f"T=4096 (the GPU line's workload) {n4096} calls in {e4096:.1f} s; "
+                      f"config 0 T=64 {n64} calls in {e64:.1f} s; BLAS threads={threads}, "
+                      f"os.cpu_count()={os.cpu_count()}",
+            "tokens_per_s_T4096": v4096, "tokens_per_s_T64": v64, "cpu_model": model,
+            "blas_threads": int(threads), "os_cpu_count": os.cpu_count()}
 
 
 COPY_BYTES = 1 << 30  # calibration copy: 1 GiB read + 1 GiB written per launch

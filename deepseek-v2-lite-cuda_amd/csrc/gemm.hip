@@ -46,6 +46,7 @@
 // weight rows are half gate rows (j) and half the matching up rows (I + j), so
 // silu(gate) * up is computed from fp32 accumulators held by the same lane.
 #include "dsk_internal.hpp"
+#include "gemm_sched.hpp"
 
 #include <algorithm>
 #include <atomic>
@@ -56,7 +57,6 @@
 namespace dsk {
 
 constexpr int kMaxGroups = 128;
-constexpr int kTileChunk = 16;  // tiles dealt to one XCD at a time
 constexpr int kLdsPerCU = 160 * 1024;
 
 // Tile configuration (build-time; tuned on MI355X).
@@ -247,25 +247,13 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void grouped_gemm_kernel
   __syncthreads();
   const int total_tiles = s_inc[G - 1];
 
-  // ---- XCD-aware persistent enumeration. Tiles (group-major, then N tile,
-  // then M tile) are dealt to the 8 XCDs in chunks of kChunk consecutive
-  // tiles (chunk c -> XCD c % 8), so every XCD gets the same mix of tile
-  // sizes, and the M tiles of one weight tile stay on one XCD. Inside an XCD,
-  // position q goes to workgroup slot q % per_xcd in round q / per_xcd:
-  // consecutive tiles run at the same time on neighbouring workgroups.
-  constexpr int kChunk = kTileChunk;
+  // ---- XCD-aware persistent enumeration (gemm_sched.hpp): tiles dealt to the
+  // 8 XCDs in chunks, so the M tiles of one weight tile stay on one XCD
   const int xcd = blockIdx.x & 7;
   const int slot = blockIdx.x >> 3;
   const int per_xcd = gridDim.x >> 3;
-  const int n_chunks = (total_tiles + kChunk - 1) / kChunk;
-  int xcd_tiles = 0;  // positions held by this XCD
-  if (xcd < n_chunks) {
-    const int mine = (n_chunks - xcd + 7) >> 3;
-    xcd_tiles = mine * kChunk;
-    if ((n_chunks - 1) % 8 == xcd) xcd_tiles -= n_chunks * kChunk - total_tiles;
-  }
-  if (slot >= xcd_tiles) return;  // uniform: no work for this workgroup
-  const int ntiles = (xcd_tiles - slot + per_xcd - 1) / per_xcd;
+  const int ntiles = sched_slot_tiles(sched_xcd_tiles(total_tiles, xcd), slot, per_xcd);
+  if (ntiles == 0) return;  // uniform: no work for this workgroup
   const int nk = p.K / BK;
   const int total = ntiles * nk;  // stages in this workgroup's stream
 
@@ -273,8 +261,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void grouped_gemm_kernel
     int g, m0, me, n0;  // rows [m0, me) of group g, output columns from n0
   };
   auto decode = [&](int t) -> Tile {
-    const int q = slot + t * per_xcd;
-    const int W = ((q / kChunk) * 8 + xcd) * kChunk + q % kChunk;
+    const int W = sched_tile_index(xcd, slot, t, per_xcd);
     int lo = 0, hi = G - 1;
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
@@ -663,19 +650,11 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void wide_gemm_kernel(GemmArgs 
   const int total_tiles = s_inc[G - 1];
 
   // ---- XCD-aware persistent enumeration (as in grouped_gemm_kernel)
-  constexpr int kChunk = kTileChunk;
   const int xcd = blockIdx.x & 7;
   const int slot = blockIdx.x >> 3;
   const int per_xcd = gridDim.x >> 3;
-  const int n_chunks = (total_tiles + kChunk - 1) / kChunk;
-  int xcd_tiles = 0;
-  if (xcd < n_chunks) {
-    const int mine = (n_chunks - xcd + 7) >> 3;
-    xcd_tiles = mine * kChunk;
-    if ((n_chunks - 1) % 8 == xcd) xcd_tiles -= n_chunks * kChunk - total_tiles;
-  }
-  if (slot >= xcd_tiles) return;
-  const int ntiles = (xcd_tiles - slot + per_xcd - 1) / per_xcd;
+  const int ntiles = sched_slot_tiles(sched_xcd_tiles(total_tiles, xcd), slot, per_xcd);
+  if (ntiles == 0) return;
   const int nk = p.K / kWideBK;  // even (K % 128 == 0, checked by the launcher)
   const int total = ntiles * nk;
 
@@ -683,8 +662,7 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void wide_gemm_kernel(GemmArgs 
     int g, m0, me, n0;
   };
   auto decode = [&](int t) -> Tile {
-    const int q = slot + t * per_xcd;
-    const int W = ((q / kChunk) * 8 + xcd) * kChunk + q % kChunk;
+    const int W = sched_tile_index(xcd, slot, t, per_xcd);
     int lo = 0, hi = G - 1;
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
@@ -1277,18 +1255,13 @@ static int launch_grouped_gemm(const GemmArgs& a, hipStream_t st) {
   allow_lds(once, reinterpret_cast<const void*>(kern), Cfg::LDS_BYTES);
   const int G = a.offsets != nullptr ? a.G : 1;
   const int64_t nt = (a.N + Cfg::OUT_N - 1) / Cfg::OUT_N;
+  // upper bound on the kernel's tile count (a group of n rows has ceil(n/BM) M tiles)
   const int64_t upper = ((int64_t)(a.M + BM - 1) / BM + (a.offsets ? G : 0)) * nt;
-  int64_t nwg = std::min<int64_t>(upper, (int64_t)num_cus());
-  nwg = std::max<int64_t>(8, (nwg + 7) / 8 * 8);
-  if (GATHER) {
-    // every workgroup's tile count must fit the LDS row table: an XCD holds
-    // at most ceil(chunks / 8) chunks of kTileChunk tiles, spread over nwg / 8
-    // workgroups
-    const int64_t chunks = (upper + kTileChunk - 1) / kTileChunk;
-    const int64_t xcd_max = (chunks + 7) / 8 * kTileChunk;
-    const int64_t per_xcd_min = (xcd_max + Cfg::ROW_TILES - 1) / Cfg::ROW_TILES;
-    nwg = std::max<int64_t>(nwg, 8 * per_xcd_min);
-  }
+  const int64_t nwg = sched_workgroups(upper, num_cus(), GATHER ? Cfg::ROW_TILES : 0);
+  // the gathered kernel stages every tile's row indices in an LDS table of
+  // ROW_TILES tiles and computes nothing if its share is larger
+  if (GATHER && (upper > INT32_MAX || sched_max_tiles((int)upper, (int)nwg) > Cfg::ROW_TILES))
+    return fail(DSK_ERR_INVALID_ARG, "grouped_gemm: a workgroup's tiles exceed the LDS row table");
   hipLaunchKernelGGL(kern, dim3((unsigned)nwg), dim3(Cfg::THREADS), Cfg::LDS_BYTES, st, a);
   return check_launch("grouped_gemm_kernel");
 }
@@ -1302,15 +1275,9 @@ static int launch_wide_gemm(const GemmArgs& a, hipStream_t st) {
   const int G = a.offsets != nullptr ? a.G : 1;
   const int64_t nt = (a.N + OUT_N - 1) / OUT_N;
   const int64_t upper = ((int64_t)(a.M + kWideBM - 1) / kWideBM + (a.offsets ? G : 0)) * nt;
-  int64_t nwg = std::min<int64_t>(upper, (int64_t)num_cus());
-  nwg = std::max<int64_t>(8, (nwg + 7) / 8 * 8);
-  if (GATHER) {
-    // every workgroup's tile count must fit the LDS row table
-    const int64_t chunks = (upper + kTileChunk - 1) / kTileChunk;
-    const int64_t xcd_max = (chunks + 7) / 8 * kTileChunk;
-    const int64_t per_xcd_min = (xcd_max + kWideRowTiles - 1) / kWideRowTiles;
-    nwg = std::max<int64_t>(nwg, 8 * per_xcd_min);
-  }
+  const int64_t nwg = sched_workgroups(upper, num_cus(), GATHER ? kWideRowTiles : 0);
+  if (GATHER && (upper > INT32_MAX || sched_max_tiles((int)upper, (int)nwg) > kWideRowTiles))
+    return fail(DSK_ERR_INVALID_ARG, "wide_gemm: a workgroup's tiles exceed the LDS row table");
   hipLaunchKernelGGL(kern, dim3((unsigned)nwg), dim3(64 * kWideWaves), kWideLdsBytes, st, a);
   return check_launch("wide_gemm_kernel");
 }

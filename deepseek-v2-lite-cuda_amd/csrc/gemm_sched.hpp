@@ -1,0 +1,76 @@
+// Persistent-grid tile schedule of the grouped GEMM kernels, shared by the
+// kernels (which decode their tiles from it) and the launchers (which size the
+// grid from it). Plain integer arithmetic, also compiled by the host compiler
+// alone for the CPU check of the schedule (tests/gemm_schedule_check.cpp).
+//
+// A launch enumerates T output tiles (group-major, then N tile, then M tile)
+// and deals them to the 8 XCDs in chunks of kTileChunk consecutive tiles:
+// chunk c goes to XCD c % 8, so every XCD gets the same mix of tile sizes and
+// the M tiles that share a weight tile stay on one XCD (one L2). Workgroup i
+// runs on XCD i % 8 in slot i / 8; inside an XCD, the XCD's q-th tile goes to
+// slot q % per_xcd in round q / per_xcd, so consecutive tiles run at the same
+// time on neighbouring workgroups.
+#pragma once
+
+#include <cstdint>
+
+#if defined(__HIPCC__)
+#define DSK_HD __host__ __device__ __forceinline__
+#else
+#define DSK_HD inline
+#endif
+
+namespace dsk {
+
+constexpr int kTileChunk = 16;  // tiles dealt to one XCD at a time
+constexpr int kXcds = 8;
+
+// Tiles held by XCD `xcd` out of `total`.
+DSK_HD int sched_xcd_tiles(int total, int xcd) {
+  const int n_chunks = (total + kTileChunk - 1) / kTileChunk;
+  if (xcd >= n_chunks) return 0;
+  int t = ((n_chunks - xcd + kXcds - 1) / kXcds) * kTileChunk;
+  if ((n_chunks - 1) % kXcds == xcd) t -= n_chunks * kTileChunk - total;  // partial last chunk
+  return t;
+}
+
+// Tiles run by workgroup slot `slot` of an XCD that holds xcd_tiles tiles over
+// per_xcd workgroups.
+DSK_HD int sched_slot_tiles(int xcd_tiles, int slot, int per_xcd) {
+  return slot >= xcd_tiles ? 0 : (xcd_tiles - slot + per_xcd - 1) / per_xcd;
+}
+
+// Global tile index of the t-th tile of (xcd, slot).
+DSK_HD int sched_tile_index(int xcd, int slot, int t, int per_xcd) {
+  const int q = slot + t * per_xcd;
+  return ((q / kTileChunk) * kXcds + xcd) * kTileChunk + q % kTileChunk;
+}
+
+// The largest number of tiles any workgroup runs (nwg a multiple of 8).
+DSK_HD int sched_max_tiles(int total, int nwg) {
+  int m = 0;
+  for (int x = 0; x < kXcds; ++x) {
+    const int t = sched_slot_tiles(sched_xcd_tiles(total, x), 0, nwg / kXcds);
+    m = t > m ? t : m;
+  }
+  return m;
+}
+
+// Workgroups (a multiple of 8, at least 8) for a launch of at most `upper`
+// tiles on `cus` compute units such that no workgroup runs more than
+// row_tiles tiles (the gathered kernels stage each tile's row indices in an
+// LDS table of row_tiles tiles). row_tiles <= 0: no limit.
+inline int64_t sched_workgroups(int64_t upper, int64_t cus, int row_tiles) {
+  int64_t nwg = upper < cus ? upper : cus;
+  nwg = (nwg + kXcds - 1) / kXcds * kXcds;
+  if (nwg < kXcds) nwg = kXcds;
+  if (row_tiles > 0) {
+    const int64_t chunks = (upper + kTileChunk - 1) / kTileChunk;
+    const int64_t xcd_max = (chunks + kXcds - 1) / kXcds * kTileChunk;
+    const int64_t per_xcd_min = (xcd_max + row_tiles - 1) / row_tiles;
+    if (nwg < kXcds * per_xcd_min) nwg = kXcds * per_xcd_min;
+  }
+  return nwg;
+}
+
+}  // namespace dsk

@@ -29,6 +29,7 @@ from .expert_prepack import (  # noqa: F401
     prepack_with_shared,
     tile_weights,
     untile_weights,
+    verify_prepack,
 )
 from .mla_cache import AbsorbedMLAWeights, LatentKVCache, mla_decode_forward  # noqa: F401
 from .moe_fused import (  # noqa: F401
@@ -44,7 +45,7 @@ __all__ = [
     "moe_gemm1_swiglu", "moe_gemm2", "rms_norm", "kv_upproj", "linear", "rope", "attn_softmax_",
     "linear_batched", "linear_split", "mla_decode_attention", "LatentKVCache", "AbsorbedMLAWeights", "mla_decode_forward",
     "prepack_experts", "prepack_with_shared", "pack_tensors", "tile_weights", "untile_weights",
-    "FusedMoELayer",
+    "verify_prepack", "FusedMoELayer",
     "fused_moe_forward", "moe_fused_forward_logits", "moe_layer_forward",
     "route_dispatch_combine", "DskError",
 ]

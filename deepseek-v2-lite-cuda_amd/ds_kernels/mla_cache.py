@@ -204,11 +204,35 @@ def mla_decode_forward(x: torch.Tensor, W: MLAWeights, cache: LatentKVCache, cos
     ops._req(b == cache.bsz, f"{op}: x has batch {b}, the cache {cache.bsz}.")
     ops._req(cache.kv_lora_rank == W.kv_lora and cache.rope_head_dim == W.rope_dim,
              f"{op}: cache widths do not match the weights.")
+    h, nope, r, vd, lora = W.n_heads, W.nope, W.rope_dim, W.v_dim, W.kv_lora
+    # everything a later step would reject is checked before the cache advances
+    w_in = W.kva.shape[1] * 16 if W.kva.dim() == 4 else W.kva.shape[1]
+    ops._req(H == w_in, f"{op}: x has hidden size {H}, the projections take {w_in}.")
+    end = cache.current_len + n
+    for t, name in ((cos, "cos"), (sin, "sin")):
+        ops._req(t.dim() == 2 and t.shape[1] == r and t.shape[0] >= end,
+                 f"{op}: {name} must be [positions >= {end}, {r}], got {tuple(t.shape)}.")
+    ops._req(n <= cache.remaining_capacity,
+             f"KV cache overflow: current_len={cache.current_len}, new_tokens={n}, "
+             f"max_seq={cache.max_seq}. Increase max_seq or reset the cache.")
     A = absorbed if absorbed is not None else AbsorbedMLAWeights.from_mla(W)
+    len0 = cache.current_len
+    rows = cache.append_slots(n)                           # [b, n, 576] slots
+    try:
+        return _decode_step(x, W, cache, rows, cos, sin, A, eps)
+    except Exception:
+        cache._len = len0      # the rows were not (all) written: do not count them
+        raise
+
+
+def _decode_step(x: torch.Tensor, W: MLAWeights, cache: LatentKVCache, rows: torch.Tensor,
+                 cos: torch.Tensor, sin: torch.Tensor, A: AbsorbedMLAWeights,
+                 eps: float) -> torch.Tensor:
+    """mla_decode_forward after the cache slots of the new tokens are reserved."""
+    b, n, H = x.shape
     h, nope, r, vd, lora = W.n_heads, W.nope, W.rope_dim, W.v_dim, W.kv_lora
     T = b * n
     x2 = x.reshape(T, H)
-    rows = cache.append_slots(n)                           # [b, n, 576] slots
     nq = h * (nope + r)
     if (b == 1 or n == 1) and W.q_kva is not None and W.q_kva.dim() == 4 and T <= 64:
         # q_proj and kv_a_proj in one launch, kv_a's rows straight into the slots

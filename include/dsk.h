@@ -98,7 +98,12 @@ int dsk_moe_scan(const int32_t* expert_counts, int32_t* expert_offsets,
  * dispatched may be NULL (index-only dispatch). Entries whose expert index is
  * outside [0,E) or whose slot falls outside [0, T*K) are skipped.
  * Replaces launch_moe_dispatch (include/moe/dispatch.h:44-57,
- * dispatch.cu:106-139) and moe_dispatch_forward (dispatch.cu:156-218). */
+ * dispatch.cu:106-139) and moe_dispatch_forward (dispatch.cu:156-218) in
+ * function, not argument for argument: this entry adds ld_x, num_experts and a
+ * sized workspace (instead of the caller-zeroed expert_cursor), takes the
+ * output `dispatched` after the three inputs rather than second, and returns a
+ * status. The Python op `moe_dispatch` keeps the reference's argument order
+ * (bindings.cu); a C caller of launch_moe_dispatch must reorder. */
 size_t dsk_moe_dispatch_workspace_size(int num_tokens, int num_experts,
                                        int top_k);
 int dsk_moe_dispatch(const dsk_bf16* x, int64_t ld_x, const int32_t* topk_idx,
@@ -113,7 +118,12 @@ int dsk_moe_dispatch(const dsk_bf16* x, int64_t ld_x, const int32_t* topk_idx,
  *                  dispatched_weights[s] * float(expert_out[s,:]) ), fp32
  * accumulation, one rounding, no float atomics. Tokens with no slot -> 0.
  * Replaces launch_moe_combine (include/moe/combine.h:41-49, combine.cu:80-93)
- * and moe_combine_forward (combine.cu:107-176). */
+ * and moe_combine_forward (combine.cu:107-176) in function, not argument for
+ * argument: the output `out` comes after token_map and dispatched_weights
+ * rather than second, num_tokens and a workspace are added, `out` needs no
+ * zero-filling by the caller, and a status is returned. The Python op
+ * `moe_combine` keeps the reference's argument order (bindings.cu); a C caller
+ * of launch_moe_combine must reorder. */
 size_t dsk_moe_combine_workspace_size(int total_slots, int num_tokens);
 int dsk_moe_combine(const dsk_bf16* expert_out, const int32_t* token_map,
                     const float* dispatched_weights, dsk_bf16* out,

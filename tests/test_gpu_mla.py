@@ -268,6 +268,34 @@ def test_decoder_layer_matches_oracle(mla_setup):
     assert max_rel_err(np32(out), ref) <= BF16_TOL
 
 
+def test_decoder_layer_matches_oracle_large_groups(mla_setup):
+    """Config 4's layer at b=2, s=512 (1024 tokens) against the fp32 oracle: the
+    MoE inside runs the T > 64 routing (route, then scan and permutation in one
+    kernel), the large-group GEMMs (routed groups of ~100 rows, shared groups of
+    1024) and the attention softmax over up to 512 causal keys.
+    Reference composition: decoder_layer.py:108-139."""
+    dm, w, W, wn = mla_setup
+    from ds_kernels import synthetic as syn
+    M = syn.moe_weights()
+    P = dm.DecoderLayerWeights.from_tensors(w, M, torch.device(DEV))
+    b, s = 2, 512
+    g = torch.Generator().manual_seed(14)
+    x = torch.randn(b, s, 2048, generator=g).to(torch.bfloat16)
+    cos, sin = dm.yarn_cos_sin(s)
+    out = dm.decoder_layer_forward(x.to(DEV), P, cos.to(DEV), sin.to(DEV))
+    p = {"in_norm": np.ones(2048, np.float32), "post_norm": np.ones(2048, np.float32),
+         "q": wn["q"], "kva": wn["kva"], "kva_norm": wn["kva_norm"], "kvb": wn["kvb"],
+         "o": wn["o"], "wg": _bf(M.wg), "gates": _bf(M.gates), "ups": _bf(M.ups),
+         "downs": _bf(M.downs), "shared": tuple(_bf(t) for t in M.shared)}
+    ref = ol.decoder_layer(np32(x), p)
+    assert out.shape == (b, s, 2048)
+    assert max_rel_err(np32(out), ref) <= BF16_TOL
+    # the layer's residual stream dominates max|ref|: check the update the layer
+    # adds (attention + MoE) on its own scale too
+    upd, rupd = np32(out) - np32(x), ref - np32(x)
+    assert max_rel_err(upd, rupd) <= 4 * BF16_TOL
+
+
 def test_config3_projection_block_full_size(mla_setup):
     """BASELINE config 3 at its full size (b=8, s=2048): every output of the
     projection block against the oracle."""

@@ -97,3 +97,32 @@ def test_append_slots_reserves_views_in_order():
     with pytest.raises(RuntimeError, match="KV cache overflow: current_len=5, new_tokens=2"):
         c.append_slots(2)
     assert c.current_len == 5
+
+
+def test_rejected_decode_step_leaves_the_cache_length():
+    """mla_decode_forward checks its inputs before it reserves cache slots, and
+    gives the slots back if a later step raises: a caller that catches the error
+    and carries on never attends over rows that were not written. The reference
+    update() advances the length only after its writes (mla_cache.py:131-143)."""
+    from ds_kernels import mla_decode_forward
+    from ds_kernels import mla as dm
+    from ds_kernels import synthetic as syn
+    W = dm.MLAWeights.from_tensors(syn.mla_weights(), torch.device("cpu"))
+    c = LatentKVCache(1, 16, device="cpu")
+    c.update(_tokens(1, 5, 0, 512), _tokens(1, 5, 1, 64))
+    cos, sin = dm.yarn_cos_sin(16)
+    cos, sin = cos.to(torch.bfloat16), sin.to(torch.bfloat16)
+    x = _tokens(1, 2, 2, 2048)
+    with pytest.raises(RuntimeError, match="cos must be"):           # table too short
+        mla_decode_forward(x, W, c, cos[:6], sin[:6])
+    with pytest.raises(RuntimeError, match="hidden size 1024"):
+        mla_decode_forward(_tokens(1, 2, 3, 1024), W, c, cos, sin)
+    c32, s32 = (t.to(torch.bfloat16) for t in dm.yarn_cos_sin(32))
+    with pytest.raises(RuntimeError, match="KV cache overflow"):
+        mla_decode_forward(_tokens(1, 12, 4, 2048), W, c, c32, s32)
+    assert c.current_len == 5
+    # valid shapes, but the tensors are on the CPU: the projection rejects them
+    # after the slots were reserved, and the reservation is undone
+    with pytest.raises(RuntimeError, match="CUDA"):
+        mla_decode_forward(x, W, c, cos, sin)
+    assert c.current_len == 5

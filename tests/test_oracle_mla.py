@@ -40,6 +40,25 @@ def test_yarn_correction_range_and_bands():
     assert ol.yarn_get_mscale(40, 0.707) / ol.yarn_get_mscale(40, 0.707) == 1.0
 
 
+def test_yarn_ramp_interior_is_linear():
+    """Inside the correction range the YaRN blend (mla.py:85-91,137-155) moves
+    linearly from extrapolation to interpolation: with the blend weight
+    t_i = (extra_i - inv_i) / (extra_i - extra_i / factor) recovered from the
+    table, t rises by the same step 1 / (hi - lo) at every index of the ramp,
+    is 0 at lo and 1 at hi. A clipped, reversed or non-linear ramp fails."""
+    lo, hi = ol.yarn_find_correction_range(32, 1, 64, 10000, 4096)
+    inv = ol.yarn_inv_freq(64, 10000.0, 40.0, 4096, 32, 1).astype(np.float64)
+    i = np.arange(32)
+    extra = 1.0 / 10000.0 ** (2 * i / 64)
+    t = (extra - inv) / (extra - extra / 40.0)
+    np.testing.assert_allclose(t[lo], 0.0, atol=1e-6)
+    np.testing.assert_allclose(t[hi], 1.0, atol=1e-6)
+    steps = np.diff(t[lo:hi + 1])
+    np.testing.assert_allclose(steps, 1.0 / (hi - lo), rtol=1e-4, atol=1e-6)
+    m = ol.yarn_linear_ramp_mask(lo, hi, 32)
+    assert m[0] == 0 and m[-1] == 1 and np.all(np.diff(m) >= 0)
+
+
 def test_yarn_tables_shape_and_symmetry():
     cos, sin = ol.yarn_cos_sin(128)
     assert cos.shape == (128, 64)
