@@ -16,6 +16,9 @@
 // rows [T*K + j*T, T*K + (j+1)*T) in token order.
 #include "dsk_internal.hpp"
 
+#include <atomic>
+#include <mutex>
+
 namespace dsk {
 
 struct FusedLayout {
@@ -238,4 +241,77 @@ extern "C" int dsk_moe_layer_forward(const dsk_bf16* x, const dsk_bf16* gate_wei
   return layer_after_gate(parts, n_parts, (int64_t)T * E, gate_bias, x, w1, w2, out, T, E, K,
                           nsh, H, I, weight_layout, topk_idx_out, topk_w_out,
                           expert_offsets_out, ws, L, stage_events, st);
+}
+
+// --------------------------------------------------- allocation-free entry --
+// dsk_moe_layer_forward_noalloc runs the same kernels as dsk_moe_layer_forward
+// with the workspace taken from `scratch`, a file-scope device array that the
+// runtime places once per GPU when it loads this library there. The host
+// never passes `scratch` itself to a kernel (in host code the name is only a
+// stand-in for the symbol): the device address is resolved once per device
+// with hipGetSymbolAddress and kept in g_scratch_addr.
+namespace dsk {
+
+constexpr size_t kNoAllocScratchBytes = DSK_NOALLOC_SCRATCH_BYTES;  // per GPU
+constexpr int kNoAllocMaxDevices = 64;
+
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+static std::atomic<void*> g_scratch_addr[kNoAllocMaxDevices];
+static std::mutex g_scratch_mu;
+
+// Device address of `scratch` on device `dev` (which must be current).
+static int scratch_address(int dev, void** out) {
+  void* p = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_addr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || p == nullptr)
+        return fail(DSK_ERR_LAUNCH, std::string("moe_layer_noalloc: hipGetSymbolAddress(scratch) "
+                                                "failed: ") + hipGetErrorString(e));
+      g_scratch_addr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return DSK_OK;
+}
+
+}  // namespace dsk
+
+extern "C" int dsk_moe_layer_forward_noalloc(const dsk_bf16* x, const dsk_bf16* gate_weight,
+                                             const float* gate_bias, const dsk_bf16* w1,
+                                             const dsk_bf16* w2, dsk_bf16* out,
+                                             int num_tokens, int num_experts, int top_k,
+                                             int n_shared_groups, int hidden,
+                                             int intermediate, int weight_layout,
+                                             int32_t* topk_idx_out, float* topk_w_out,
+                                             int32_t* expert_offsets_out,
+                                             void* const* stage_events, void* stream) {
+  const int T = num_tokens, E = num_experts, K = top_k, nsh = n_shared_groups;
+  const int H = hidden, I = intermediate;
+  int rc = check_layer_args("moe_layer_noalloc", T, E, K, nsh, H, I, weight_layout);
+  if (rc) return rc;
+  const size_t need = dsk_moe_layer_workspace_size(T, E, K, nsh, H, I);
+  DSK_REQUIRE(need <= kNoAllocScratchBytes, DSK_ERR_WORKSPACE,
+              "moe_layer_noalloc: this layer needs " + std::to_string(need) +
+                  " bytes of scratch, more than the " + std::to_string(kNoAllocScratchBytes) +
+                  " bytes of the library's static per-GPU scratch; use dsk_moe_layer_forward "
+                  "with a caller-allocated workspace");
+  if (T == 0) return DSK_OK;
+  int dev = -1;
+  DSK_REQUIRE(hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kNoAllocMaxDevices,
+              DSK_ERR_LAUNCH, "moe_layer_noalloc: no usable current device");
+  hipStream_t st = as_stream(stream);
+  if (st != nullptr) {
+    int sdev = -1;
+    DSK_REQUIRE(hipStreamGetDevice(st, &sdev) == hipSuccess && sdev == dev, DSK_ERR_INVALID_ARG,
+                "moe_layer_noalloc: the stream must belong to the current device");
+  }
+  void* ws = nullptr;
+  if ((rc = scratch_address(dev, &ws))) return rc;
+  return dsk_moe_layer_forward(x, gate_weight, gate_bias, w1, w2, out, T, E, K, nsh, H, I,
+                               weight_layout, topk_idx_out, topk_w_out, expert_offsets_out, ws,
+                               kNoAllocScratchBytes, stage_events, stream);
 }

@@ -57,6 +57,8 @@ SIGNATURES = {
     "dsk_moe_layer_workspace_size": (_SZ, [_I, _I, _I, _I, _I, _I]),
     "dsk_moe_layer_forward": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P,
                                    _P, _P, _SZ, _P, _P]),
+    "dsk_moe_layer_forward_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I,
+                                           _P, _P, _P, _P, _P]),
 }
 
 

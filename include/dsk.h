@@ -350,6 +350,32 @@ int dsk_moe_layer_forward(const dsk_bf16* x, const dsk_bf16* gate_weight,
                           size_t workspace_bytes, void* const* stage_events,
                           void* stream);
 
+/* ------------------------------------------ allocation-free fused MoE layer --
+ * dsk_moe_layer_forward without the workspace argument: the scratch it needs
+ * (routing planes, permutation, the [S, I] and [S, H] intermediates) lives in
+ * a static per-GPU device array of DSK_NOALLOC_SCRATCH_BYTES inside this
+ * library, so the call itself allocates nothing. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Limit: layers whose dsk_moe_layer_workspace_size exceeds
+ * DSK_NOALLOC_SCRATCH_BYTES are rejected with DSK_ERR_WORKSPACE (at the
+ * DeepSeek-V2-Lite shapes E=64, K=6, 2 shared groups, H=2048, I=1408 that
+ * admits T <= 128, the decode sizes). The stream must belong to the current
+ * device; the first call on a device resolves the array's device address.
+ * Every call on one GPU shares that GPU's array (no state is carried from one
+ * call to the next): calls that overlap on one GPU, e.g. on two streams, race
+ * and must be serialised by the caller. Arguments otherwise as for
+ * dsk_moe_layer_forward. */
+#define DSK_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
+int dsk_moe_layer_forward_noalloc(const dsk_bf16* x, const dsk_bf16* gate_weight,
+                                  const float* gate_bias, const dsk_bf16* w1,
+                                  const dsk_bf16* w2, dsk_bf16* out, int num_tokens,
+                                  int num_experts, int top_k, int n_shared_groups,
+                                  int hidden, int intermediate, int weight_layout,
+                                  int32_t* topk_idx_out, float* topk_w_out,
+                                  int32_t* expert_offsets_out,
+                                  void* const* stage_events, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
