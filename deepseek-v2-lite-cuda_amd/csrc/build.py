@@ -52,6 +52,6 @@ def build(out: str = DEFAULT_OUT, extra: list[str] | None = None, verbose: bool 
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--out", default=DEFAULT_OUT)
-    args = ap.parse_args()
-    path = build(args.out, verbose=True)
+    args, extra = ap.parse_known_args()  # anything else is passed to hipcc (e.g. -D options)
+    path = build(args.out, extra=extra, verbose=True)
     print("built", path)
