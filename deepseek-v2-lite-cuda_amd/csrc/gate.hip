@@ -144,12 +144,15 @@ __global__ __launch_bounds__(64) void gate_parts_kernel(
   }
 }
 
-// K slices for the partial gate sums: enough single-wave workgroups to reach
-// most CUs at decode sizes, one plane when the token blocks already do.
+// K slices for the partial gate sums: more single-wave workgroups at decode
+// sizes, one plane when the token blocks already cover the CUs. At most 4: the
+// route kernel's loads of the planes sit on the decode step's critical path,
+// and 4 planes (8 K steps x 4 per slice) measured 0.6-1.7 us faster per step
+// than 16 at T = 1..64 (the gate itself is latency-bound either way).
 int gate_parts_count(int T, int E, int H) {
   const int blocks = ((T + 31) / 32) * ((E + 31) / 32);
   int n = 512 / blocks;
-  n = n < 1 ? 1 : (n > 16 ? 16 : n);  // the route kernel adds at most 16 planes
+  n = n < 1 ? 1 : (n > 4 ? 4 : n);
   return n > H / 16 ? H / 16 : n;
 }
 
