@@ -220,7 +220,16 @@ def bench_mla(dsk, syn, torch, ev, reps=20, warmup=5):
     t_kvb = timed(lambda: dsk.kv_upproj(latent, W.kvb))      # tiled weight (the block's)
     kvb_rm = dsk.untile_weights(W.kvb[None])[0].contiguous()
     t_kvb_rm = timed(lambda: dsk.kv_upproj(latent, kvb_rm))  # reference layout
-    t_block = timed(lambda: dm.mla_projections(x, W, cos, sin))
+    # the block as the reference computes it (q, k, v; the latent norm riding the
+    # q/kv_a and kv_b epilogues), and beside it with the norm as a separate pass
+    t_block = timed(lambda: dm.mla_projections(x, W, cos, sin, with_latent=False))
+    import dataclasses
+    W_sep = dataclasses.replace(W, kvb_w=None)
+    t_block_sep = timed(lambda: dm.mla_projections(x, W_sep, cos, sin))
+    t_qkva = timed(lambda: dsk.linear(x, W.q_kva))
+    t_qkva_sq = timed(lambda: dsk.linear_rowsq(x, W.q_kva, 3072, 3584))
+    _, ss = dsk.linear_rowsq(x, W.q_kva, 3072, 3584)
+    t_kvb_rs = timed(lambda: dsk.linear_rowscale(kva[..., :512], W.kvb_w, ss, 512))
     norm_bytes = 2 * rows * 512 * 2 + 512 * 4
     rope_bytes = 2 * (rows * 16 * 64 * 2) + 2 * (rows * 64 * 2) + 2 * (s * 64 * 2)
     kvb_flops = 2.0 * rows * 512 * 4096
@@ -231,6 +240,11 @@ def bench_mla(dsk, syn, torch, ev, reps=20, warmup=5):
             "shape": "b=8, s=2048: q 2048->3072, kv_a 2048->576, rms_norm(512, strided), "
                      "kv_b 512->4096, rope(q 16 heads + k, 64 dims)",
             "block_ms": t_block, "tokens_per_s": rows / (t_block * 1e-3),
+            "block_ms_norm_as_separate_pass": t_block_sep,
+            "latent_norm_in_epilogues": {
+                "q_kva_us": t_qkva * 1e3, "q_kva_with_row_sumsq_us": t_qkva_sq * 1e3,
+                "kv_b_us": t_kvb * 1e3, "kv_b_with_row_scale_us": t_kvb_rs * 1e3,
+                "rms_norm_pass_us": t_norm * 1e3},
             "rms_norm": {"us": t_norm * 1e3, "algorithmic_bytes": norm_bytes,
                          "GB/s": gbs(norm_bytes, t_norm),
                          "frac_of_8TB/s": gbs(norm_bytes, t_norm) / PEAK_HBM_GBS},
@@ -243,7 +257,7 @@ def bench_mla(dsk, syn, torch, ev, reps=20, warmup=5):
                           "GB/s": gbs(kvb_bytes, t_kvb), "weight_layout": "fragment-tiled",
                           "us_row_major_weight": t_kvb_rm * 1e3},
         }}
-    del q, kva, latent, k_pe
+    del q, kva, latent, k_pe, ss
     # config 4: the decoder layer at 4 x 2048
     P = dm.DecoderLayerWeights.from_tensors(syn.mla_weights(), syn.moe_weights(), dev)
     b4 = 4

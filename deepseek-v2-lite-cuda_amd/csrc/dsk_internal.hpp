@@ -29,6 +29,20 @@ struct GemmArgs {
   uint16_t* C2;            // skinny kernel, optional: output columns n >= n_split go to
   int64_t ldc2;            // C2[m * ldc2 + n - n_split] instead of C (n_split % 64 == 0)
   int n_split;
+  // Row statistics in the epilogue of the one-wave-per-SIMD kernel (G = 1, no
+  // SwiGLU, no gather), optional:
+  //   rowsq_out[(n0 - rowsq_c0) / 256 * ld_rowsq + m] = sum over the 256 output
+  //   columns n0.. of tile n0 (inside [rowsq_c0, rowsq_c1)) of bf16(C[m, n])^2;
+  //   rowscale_ss != NULL: C[m, :] *= rsqrt(sum_p rowscale_ss[p * ld_rowscale + m]
+  //   / rowscale_cols + rowscale_eps), p < rowscale_parts (an RMS norm of the A
+  //   rows whose weight is folded into B).
+  float* rowsq_out;
+  int64_t ld_rowsq;
+  int rowsq_c0, rowsq_c1;
+  const float* rowscale_ss;
+  int64_t ld_rowscale;
+  int rowscale_parts, rowscale_cols;
+  float rowscale_eps;
 };
 
 int run_gemm(const GemmArgs& a, bool swiglu, hipStream_t st);

@@ -591,6 +591,7 @@ constexpr int kWideStageBytes = kWideBM * kWideBK * 2;  // 32 KB
 constexpr int kWideRingBytes = kWideRing * kWideStageBytes;
 constexpr int kWideRowTiles = (kLdsPerCU - kWideRingBytes - 4096) / (kWideBM * 4);
 constexpr int kWideLdsBytes = kWideRingBytes + kWideRowTiles * kWideBM * 4;
+constexpr int kRowScaleParts = 2;  // sum-of-squares partials an RMS row scale adds up
 
 // Global->LDS DMA of 16 bytes per lane (1 KB per wave to lds_addr) from
 // base + voff, as inline asm. The compiler's wait-count bookkeeping does not
@@ -816,6 +817,22 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void wide_gemm_kernel(GemmArgs 
     // sit behind uniform branches. A copy of the K loop per block count would
     // merge 256 live accumulators at the branch and overflow the registers.
     const int tma = max(1, min(TM, (ct.me - ct.m0 + 31) / 32));
+    // Sum-of-squares partials of this tile's token rows (row ct.m0 + 32 i +
+    // lane % 32) for the RMS row scale, loaded now and only added up in the
+    // epilogue: a use here would make the wave wait for every DMA issued
+    // before these loads (the wait counts complete in order).
+    float rsc[TM][kRowScaleParts];
+    if constexpr (!SWIGLU && !GATHER) {
+      if (p.rowscale_ss != nullptr) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          const int m = min(ct.m0 + 32 * i + (lane & 31), p.M - 1);
+#pragma unroll
+          for (int q = 0; q < kRowScaleParts; ++q)
+            rsc[i][q] = p.rowscale_ss[min(q, p.rowscale_parts - 1) * p.ld_rowscale + m];
+        }
+      }
+    }
     {
       // one stage: K steps 0..3 on weight set SET; the barrier before the last
       // step publishes the next stage's tokens and frees this stage's slot
@@ -883,9 +900,27 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void wide_gemm_kernel(GemmArgs 
       const int r32 = lane & 31, h = lane >> 5;
       const int col0 = SWIGLU ? ct.n0 + 32 * wave : ct.n0 + 64 * wave;  // this wave's columns
       const int rl = lane / CHUNKS, cl = lane % CHUNKS;
+      constexpr bool kRowOps = !SWIGLU && !GATHER;
+      const bool scale_rows = kRowOps && p.rowscale_ss != nullptr;
+      // whole tile inside the sum-of-squares column range (256-aligned bounds)
+      const bool sum_rows = kRowOps && p.rowsq_out != nullptr && ct.n0 >= p.rowsq_c0 &&
+                            ct.n0 < p.rowsq_c1;
+      // per-wave row partials of the sums of squares, behind the ring (the
+      // gathered kernels' row table, unused here)
+      float* s_ss = reinterpret_cast<float*>(lds + kWideRingBytes / 2);
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         if (i >= tma) continue;
+        float rs = 1.f;
+        if constexpr (kRowOps) {
+          if (scale_rows) {
+            float ss = rsc[i][0];
+#pragma unroll
+            for (int q = 1; q < kRowScaleParts; ++q)
+              if (q < p.rowscale_parts) ss += rsc[i][q];
+            rs = rsqrtf(ss * (1.f / p.rowscale_cols) + p.rowscale_eps);
+          }
+        }
 #pragma unroll
         for (int j = 0; j < JN; ++j) {
 #pragma unroll
@@ -896,7 +931,7 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void wide_gemm_kernel(GemmArgs 
               if constexpr (SWIGLU)
                 v[c] = silu_f(acc_read(acc[0][i][4 * qg + c])) * acc_read(acc[1][i][4 * qg + c]);
               else
-                v[c] = acc_read(acc[j][i][4 * qg + c]);
+                v[c] = acc_read(acc[j][i][4 * qg + c]) * rs;
             }
             u32x2_t o;
             o[0] = pack_bf16x2(v[0], v[1]);
@@ -916,10 +951,39 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void wide_gemm_kernel(GemmArgs 
           const int col = col0 + 8 * cl;
           if (m < ct.me && col < p.N)
             *reinterpret_cast<u32x4_t*>(p.C + (int64_t)m * p.ldc + col) = d;
+          if constexpr (kRowOps) {
+            if (sum_rows) {
+              // squares of the stored (bf16) values, summed over the row's 8
+              // lanes (quad swaps, then the half-row mirror)
+              float sq = 0.f;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const float lo = bf16lo(d[e]), hi = bf16hi(d[e]);
+                sq = fmaf(lo, lo, sq);
+                sq = fmaf(hi, hi, sq);
+              }
+              sq += dpp_f32<0xB1>(0.f, sq);
+              sq += dpp_f32<0x4E>(0.f, sq);
+              sq += dpp_f32<0x141>(0.f, sq);
+              if (cl == 0) s_ss[wave * kWideBM + 32 * i + rr] = sq;
+            }
+          }
         }
       }
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's staging reads done
       lds_barrier();                       // before the next DMA into the slot
+      if constexpr (kRowOps) {
+        if (sum_rows) {
+          // the tile's row sums, the four waves' column ranges added in order
+          const int t = tid;  // 256 threads, one token row each
+          const int m = ct.m0 + t;
+          if (t < 32 * tma && m < ct.me) {
+            const float ss = ((s_ss[t] + s_ss[kWideBM + t]) + s_ss[2 * kWideBM + t]) +
+                             s_ss[3 * kWideBM + t];
+            p.rowsq_out[(int64_t)((ct.n0 - p.rowsq_c0) / (64 * kWideWaves)) * p.ld_rowsq + m] = ss;
+          }
+        }
+      }
     }
 #pragma unroll
     for (int j = 0; j < TN; ++j)
@@ -1356,6 +1420,26 @@ static int run_gemm_t(const GemmArgs& a, hipStream_t st) {
 
 int run_gemm(const GemmArgs& a, bool swiglu, hipStream_t st) {
   if (a.M == 0) return DSK_OK;
+  if (a.rowsq_out != nullptr || a.rowscale_ss != nullptr) {
+    // row statistics live in the one-wave-per-SIMD kernel's epilogue only
+    DSK_REQUIRE(a.b_tiled && !swiglu && a.a_rows == nullptr && a.offsets == nullptr &&
+                    a.K % (2 * kWideBK) == 0 && aligned16(a.C) && a.ldc % 8 == 0,
+                DSK_ERR_INVALID_ARG,
+                "linear row statistics: need a tiled weight, K % 128 == 0 and 16-byte aligned "
+                "output rows");
+    DSK_REQUIRE(a.rowsq_out == nullptr ||
+                    (a.rowsq_c0 >= 0 && a.rowsq_c0 < a.rowsq_c1 && a.rowsq_c1 <= a.N &&
+                     a.rowsq_c0 % 256 == 0 && a.rowsq_c1 % 256 == 0 && a.ld_rowsq >= a.M),
+                DSK_ERR_INVALID_ARG,
+                "linear_rowsq: the column range must be 256-aligned inside [0, N) and "
+                "ld_rowsq >= M");
+    DSK_REQUIRE(a.rowscale_ss == nullptr ||
+                    (a.rowscale_parts >= 1 && a.rowscale_parts <= kRowScaleParts &&
+                     a.rowscale_cols > 0 && a.ld_rowscale >= a.M),
+                DSK_ERR_INVALID_ARG,
+                "linear_rowscale: need 1 or 2 parts, cols > 0 and ld_rowscale >= M");
+    return launch_wide_gemm<false, false>(a, st);
+  }
   const bool g = a.a_rows != nullptr;
   if (a.b_tiled) {
     if (swiglu) return g ? run_gemm_t<true, true, true>(a, st) : run_gemm_t<true, false, true>(a, st);
@@ -1478,6 +1562,45 @@ extern "C" int dsk_linear_ex(const dsk_bf16* x, int64_t ld_x, const dsk_bf16* w,
   if (rc) return rc;
   DSK_REQUIRE(ld_out >= N, DSK_ERR_INVALID_ARG, "linear: ld_out < N");
   return run_gemm(a, false, as_stream(stream));
+}
+
+static int linear_rowstats(const char* who, const dsk_bf16* x, int64_t ld_x,
+                           const dsk_bf16* w_tiled, dsk_bf16* out, int64_t ld_out, int M, int K,
+                           int N, GemmArgs& a, void* stream) {
+  DSK_REQUIRE(M >= 0, DSK_ERR_INVALID_ARG, std::string(who) + ": M < 0");
+  if (M == 0) return DSK_OK;
+  a.A = x; a.lda = ld_x;
+  a.B = w_tiled; a.ldb = K; a.b_group_stride = 0;
+  a.C = out; a.ldc = ld_out;
+  a.offsets = nullptr; a.G = 1;
+  a.M = M; a.N = N; a.K = K;
+  a.b_tiled = 1;
+  int rc = validate_gemm(a, who);
+  if (rc) return rc;
+  DSK_REQUIRE(ld_out >= N, DSK_ERR_INVALID_ARG, std::string(who) + ": ld_out < N");
+  return run_gemm(a, false, as_stream(stream));
+}
+
+extern "C" int dsk_linear_rowsq(const dsk_bf16* x, int64_t ld_x, const dsk_bf16* w_tiled,
+                                dsk_bf16* out, int64_t ld_out, int M, int K, int N,
+                                float* row_sumsq, int64_t ld_rowsq, int col_begin, int col_end,
+                                void* stream) {
+  DSK_REQUIRE(row_sumsq != nullptr, DSK_ERR_NULL_PTR, "linear_rowsq: row_sumsq is NULL");
+  GemmArgs a{};
+  a.rowsq_out = row_sumsq; a.ld_rowsq = ld_rowsq;
+  a.rowsq_c0 = col_begin; a.rowsq_c1 = col_end;
+  return linear_rowstats("linear_rowsq", x, ld_x, w_tiled, out, ld_out, M, K, N, a, stream);
+}
+
+extern "C" int dsk_linear_rowscale(const dsk_bf16* x, int64_t ld_x, const dsk_bf16* w_tiled,
+                                   dsk_bf16* out, int64_t ld_out, int M, int K, int N,
+                                   const float* row_sumsq, int64_t ld_rowsq, int n_parts,
+                                   int n_cols, float eps, void* stream) {
+  DSK_REQUIRE(row_sumsq != nullptr, DSK_ERR_NULL_PTR, "linear_rowscale: row_sumsq is NULL");
+  GemmArgs a{};
+  a.rowscale_ss = row_sumsq; a.ld_rowscale = ld_rowsq;
+  a.rowscale_parts = n_parts; a.rowscale_cols = n_cols; a.rowscale_eps = eps;
+  return linear_rowstats("linear_rowscale", x, ld_x, w_tiled, out, ld_out, M, K, N, a, stream);
 }
 
 extern "C" int dsk_linear_split(const dsk_bf16* x, int64_t ld_x, const dsk_bf16* w_tiled,

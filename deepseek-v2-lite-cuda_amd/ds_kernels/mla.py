@@ -76,6 +76,9 @@ class MLAWeights:
     # optional [q rows; kva rows] in one matrix (q and kva then view into it),
     # so that the prefill projections run as one GEMM launch
     q_kva: Optional[torch.Tensor] = None
+    # optional kv_b weight with the latent norm weight folded into its input
+    # columns (tiled), for the RMSNorm carried by the projection epilogues
+    kvb_w: Optional[torch.Tensor] = None
     n_heads: int = 16
     nope: int = 128
     rope_dim: int = 64
@@ -95,9 +98,13 @@ class MLAWeights:
         nq = w["q"].shape[0]
         q_kva = bf(torch.cat([w["q"], w["kva"]]))
         split = nq // 32 if tiled else nq
+        norm = w["kva_norm"].to(torch.float32)
+        # kv_b(w * xhat) = (kv_b * w) xhat: the norm weight scales kv_b's input
+        # columns (rounded to bf16 once)
+        kvb_w = bf(w["kvb"].to(torch.float32) * norm[None, :]) if tiled else None
         return MLAWeights(q=q_kva[:split], kva=q_kva[split:],
-                          kva_norm=w["kva_norm"].to(device=device, dtype=torch.float32),
-                          kvb=bf(w["kvb"]), o=bf(w["o"]), q_kva=q_kva)
+                          kva_norm=norm.to(device=device),
+                          kvb=bf(w["kvb"]), o=bf(w["o"]), q_kva=q_kva, kvb_w=kvb_w)
 
     @property
     def softmax_scale(self) -> float:
@@ -108,16 +115,28 @@ class MLAWeights:
 
 # ------------------------------------------------------------- projections --
 def mla_projections(x: torch.Tensor, W: MLAWeights, cos: torch.Tensor, sin: torch.Tensor,
-                    eps: float = 1e-6):
+                    eps: float = 1e-6, with_latent: bool = True):
     """The projection block of DeepSeekMLA.forward (mla.py:318-352, BASELINE
     config 3). x: bf16 [b, s, H]; cos/sin: bf16 [s, rope_dim] for positions 0..s-1.
     Returns (q_nope [b,h,s,nope], q_rot [b,h,s,r], k_nope [b,h,s,nope],
     v [b,h,s,v], k_rot [b,1,s,r], latent_normed [b,s,kv_lora]); q_nope, k_nope
-    and v are strided views of the projection outputs."""
+    and v are strided views of the projection outputs.
+
+    With the merged q/kv_a weight and the folded kv_b weight (MLAWeights.from_tensors
+    with tiled weights), the latent RMSNorm rides the projections' epilogues: the
+    q/kv_a GEMM also returns each row's sum of squares over the 512 latent
+    columns, and kv_b runs on the raw latent with the row scale applied to its
+    outputs, so the normalised latent is never materialised. latent_normed
+    (the reference module's intermediate, not an output of the block) is then
+    computed by the rms_norm kernel only if with_latent; otherwise it is None."""
     b, s, _ = x.shape
     h, nope, r, vd, lora = W.n_heads, W.nope, W.rope_dim, W.v_dim, W.kv_lora
     nq = h * (nope + r)
-    if W.q_kva is not None:
+    fused_norm = W.q_kva is not None and W.kvb_w is not None and nq % 256 == 0 and lora % 256 == 0
+    if fused_norm:
+        y, ss = ops.linear_rowsq(x, W.q_kva, nq, nq + lora)            # [b,s,3072+576], [2, b*s]
+        q, kva = y[..., :nq], y[..., nq:]
+    elif W.q_kva is not None:
         # one GEMM for both projections (q_proj alone leaves no partial round of
         # tiles for kv_a's 576 columns to fill); q and kva are column slices
         y = ops.linear(x, W.q_kva)                                     # [b,s,3072+576]
@@ -125,8 +144,13 @@ def mla_projections(x: torch.Tensor, W: MLAWeights, cos: torch.Tensor, sin: torc
     else:
         q, kva = ops.linear(x, W.q), ops.linear(x, W.kva)
     q = q.view(b, s, h, nope + r).transpose(1, 2)                      # [b,h,s,192] view
-    latent = ops.rms_norm(kva[..., :lora], W.kva_norm, eps)            # strided rows, no copy
-    kv = ops.kv_upproj(latent, W.kvb).view(b, s, h, nope + vd).transpose(1, 2)
+    if fused_norm:
+        kv = ops.linear_rowscale(kva[..., :lora], W.kvb_w, ss, lora, eps)
+        kv = kv.view(b, s, h, nope + vd).transpose(1, 2)
+        latent = ops.rms_norm(kva[..., :lora], W.kva_norm, eps) if with_latent else None
+    else:
+        latent = ops.rms_norm(kva[..., :lora], W.kva_norm, eps)        # strided rows, no copy
+        kv = ops.kv_upproj(latent, W.kvb).view(b, s, h, nope + vd).transpose(1, 2)
     k_pe = kva[..., lora:].view(b, s, 1, r).transpose(1, 2)           # [b,1,s,64] view
     cb = cos.to(torch.bfloat16)[None, None].expand(b, 1, s, r)         # batch stride 0
     sb = sin.to(torch.bfloat16)[None, None].expand(b, 1, s, r)
@@ -144,7 +168,7 @@ def mla_forward(x: torch.Tensor, W: MLAWeights, cos: torch.Tensor, sin: torch.Te
     pass of attn_softmax_.
     x: bf16 [b, s, H] -> bf16 [b, s, H]."""
     b, s, H = x.shape
-    q_nope, q_rot, k_nope, v, k_rot, _ = mla_projections(x, W, cos, sin, eps)
+    q_nope, q_rot, k_nope, v, k_rot, _ = mla_projections(x, W, cos, sin, eps, with_latent=False)
     h, nope, r = W.n_heads, W.nope, W.rope_dim
     q = torch.cat([q_nope, q_rot], dim=-1)                             # [b,h,s,192]
     # K^T built in place, contiguous (one pass instead of a cat and a transposed copy)

@@ -317,6 +317,57 @@ def linear(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor = None) -> t
     return out if given else out.view(*x.shape[:-1], N)
 
 
+def _rowstat_operands(op: str, x: torch.Tensor, weight: torch.Tensor):
+    _req(x.is_cuda and weight.is_cuda, f"{op}: tensors must be CUDA tensors.")
+    _req(x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16, f"{op}: bfloat16 only.")
+    K = x.shape[-1]
+    _req(weight.is_contiguous() and weight.dim() == 4 and tuple(weight.shape[2:]) == (64, 8)
+         and weight.shape[1] * 16 == K, f"{op}: weight must be fragment-tiled [N/32, {K // 16}, 64, 8].")
+    x2 = x.reshape(-1, K)
+    _req(x2.stride(-1) == 1, f"{op}: last dim of x must be contiguous.")
+    return x2, K, weight.shape[0] * 32
+
+
+def linear_rowsq(x: torch.Tensor, weight: torch.Tensor, col_begin: int, col_end: int):
+    """(x @ weight^T, row_sumsq): the projection (tiled weight) and, per output
+    row, the sum of squares of its bf16 outputs in columns [col_begin, col_end),
+    as fp32 partials [(col_end - col_begin) / 256, rows] (one per 256 columns)."""
+    op = "linear_rowsq"
+    x2, K, N = _rowstat_operands(op, x, weight)
+    M = x2.shape[0]
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    _req(col_begin % 256 == 0 and col_end % 256 == 0 and 0 <= col_begin < col_end <= N,
+         f"{op}: the column range must be 256-aligned inside [0, {N}).")
+    ss = torch.empty(((col_end - col_begin) // 256, M), dtype=torch.float32, device=x.device)
+    if M:
+        with torch.cuda.device(x.device):
+            check(lib.dsk_linear_rowsq(x2.data_ptr(), x2.stride(0), weight.data_ptr(),
+                                       out.data_ptr(), N, M, K, N, ss.data_ptr(), M, col_begin,
+                                       col_end, stream_handle(x.device)), op)
+    return out.view(*x.shape[:-1], N), ss
+
+
+def linear_rowscale(x: torch.Tensor, weight: torch.Tensor, row_sumsq: torch.Tensor,
+                    n_cols: int, eps: float = 1e-6) -> torch.Tensor:
+    """rsqrt(row_sumsq.sum(0) / n_cols + eps)[:, None] * (x @ weight^T): an RMS
+    norm of x's rows (statistics from linear_rowsq) applied in the epilogue of
+    the projection whose weight carries the norm weight per input column."""
+    op = "linear_rowscale"
+    x2, K, N = _rowstat_operands(op, x, weight)
+    M = x2.shape[0]
+    _req(row_sumsq.is_cuda and row_sumsq.dtype == torch.float32 and row_sumsq.dim() == 2
+         and row_sumsq.shape[1] == M and row_sumsq.is_contiguous(),
+         f"{op}: row_sumsq must be a contiguous float32 [parts, {M}] CUDA tensor.")
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    if M:
+        with torch.cuda.device(x.device):
+            check(lib.dsk_linear_rowscale(x2.data_ptr(), x2.stride(0), weight.data_ptr(),
+                                          out.data_ptr(), N, M, K, N, row_sumsq.data_ptr(), M,
+                                          row_sumsq.shape[0], int(n_cols), float(eps),
+                                          stream_handle(x.device)), op)
+    return out.view(*x.shape[:-1], N)
+
+
 def linear_split(x: torch.Tensor, weight: torch.Tensor, out0: torch.Tensor,
                  out1: torch.Tensor) -> None:
     """x[M, K] @ weight^T with columns [0, n0) written to out0 [M, n0] and the

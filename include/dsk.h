@@ -188,6 +188,32 @@ int dsk_linear_ex(const dsk_bf16* x, int64_t ld_x, const dsk_bf16* w,
                   int weight_layout, dsk_bf16* out, int64_t ld_out, int M,
                   int K, int N, void* stream);
 
+/* ------------------------------------- RMSNorm carried by projection epilogues --
+ * The latent RMSNorm of the MLA projection block (mla.py:318-346: kv_a ->
+ * RMSNorm(512) -> kv_b) moved into the two projections' epilogues, so the
+ * normalised latent is never written or read:
+ *   dsk_linear_rowsq:    out = x @ w^T (as dsk_linear_ex, tiled w), and for
+ *     every output row m the sum of squares of its bf16 outputs in columns
+ *     [col_begin, col_end) (256-aligned), as one fp32 partial per 256 columns:
+ *     row_sumsq[p * ld_rowsq + m], p < (col_end - col_begin) / 256.
+ *   dsk_linear_rowscale: out[m, :] = r_m * (x @ w^T)[m, :] with
+ *     r_m = rsqrt(sum_{p < n_parts} row_sumsq[p * ld_rowsq + m] / n_cols + eps),
+ *     n_parts 1 or 2 (up to 512 normalised columns).
+ * With x the raw latent (a strided view of kv_a's output) and w = kv_b's
+ * weight times the norm weight per input column, dsk_linear_rowscale is
+ * kv_b(RMSNorm(x)) to fp32 rounding (one bf16 rounding instead of the
+ * reference's two). Tiled weights only; K % 128 == 0; 16-byte aligned output
+ * rows. The reference has no counterpart: it runs rms_norm (rms_norm.cu) and
+ * kv_upproj (kv_upproj.cu) as separate passes. */
+int dsk_linear_rowsq(const dsk_bf16* x, int64_t ld_x, const dsk_bf16* w_tiled,
+                     dsk_bf16* out, int64_t ld_out, int M, int K, int N,
+                     float* row_sumsq, int64_t ld_rowsq, int col_begin,
+                     int col_end, void* stream);
+int dsk_linear_rowscale(const dsk_bf16* x, int64_t ld_x, const dsk_bf16* w_tiled,
+                        dsk_bf16* out, int64_t ld_out, int M, int K, int N,
+                        const float* row_sumsq, int64_t ld_rowsq, int n_parts,
+                        int n_cols, float eps, void* stream);
+
 /* --------------------------------------------------------------- rms_norm --
  * y = w * x * rsqrt(mean(x^2) + eps), fp32 math, one rounding of the output.
  * bf16 in/out with fp32 weight: replaces launch_rms_norm

@@ -276,3 +276,24 @@ int main(void) {
                     "-Wl,-rpath," + libdir], check=True)
     out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
     assert out.returncode == 0 and out.stdout.strip() == "ok", (out.returncode, out.stderr)
+
+
+def test_linear_row_statistics_validation(dsk):
+    """The epilogue-RMSNorm pair rejects bad column ranges, missing statistics and
+    empty reductions before any launch."""
+    lib = dsk.lib
+    # x, ld_x, w, out, ld_out, M, K, N, row_sumsq, ld_rowsq, c0, c1, stream
+    def rowsq(c0=3072, c1=3584, ss=16, ld=8):
+        return lib.dsk_linear_rowsq(16, 2048, 16, 16, 3648, 8, 2048, 3648, ss, ld, c0, c1, None)
+    assert rowsq(ss=None) == 2 and "row_sumsq" in _err(dsk)
+    assert rowsq(c0=3000) == 1 and "256-aligned" in _err(dsk)
+    assert rowsq(c1=3840) == 1 and "256-aligned" in _err(dsk)
+    assert rowsq(ld=4) == 1 and "ld_rowsq" in _err(dsk)
+    # x, ld_x, w, out, ld_out, M, K, N, row_sumsq, ld_rowsq, n_parts, n_cols, eps, stream
+    def rowscale(parts=2, cols=512, k=512):
+        return lib.dsk_linear_rowscale(16, 576, 16, 16, 4096, 8, k, 4096, 16, 8, parts, cols,
+                                       1e-6, None)
+    assert rowscale(parts=0) == 1 and "parts" in _err(dsk)
+    assert rowscale(parts=3) == 1 and "parts" in _err(dsk)
+    assert rowscale(cols=0) == 1 and "cols" in _err(dsk)
+    assert rowscale(k=64) == 1 and "K % 128" in _err(dsk)

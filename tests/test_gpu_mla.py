@@ -170,6 +170,77 @@ def test_kv_upproj_tiled_weight(dsk, rows):
     assert max_rel_err(np32(out), ref) <= BF16_TOL
 
 
+@pytest.mark.parametrize("M", [1, 300, 4096])
+def test_linear_rowsq_matches_torch(dsk, M):
+    """q/kv_a projection with the latent rows' sums of squares from its epilogue:
+    the output is bit-identical to the plain tiled projection, and each 256-column
+    partial equals the fp64 sum of squares of those bf16 outputs to fp32 rounding
+    (1e-5). Columns [3072, 3584) of a 3648-wide output, as in config 3."""
+    K, N, c0, c1 = 2048, 3648, 3072, 3584
+    g = torch.Generator().manual_seed(M + 5)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    wt = dsk.tile_weights(w[None])[0].to(DEV)
+    out, ss = dsk.linear_rowsq(x, wt, c0, c1)
+    assert torch.equal(out, dsk.linear(x, wt))
+    assert tuple(ss.shape) == ((c1 - c0) // 256, M)
+    o64 = out.double().cpu()
+    ref = torch.stack([(o64[:, c0 + 256 * p:c0 + 256 * (p + 1)] ** 2).sum(1)
+                       for p in range((c1 - c0) // 256)])
+    np.testing.assert_allclose(ss.double().cpu().numpy(), ref.numpy(), rtol=F32_TOL, atol=0)
+    out2, ss2 = dsk.linear_rowsq(x, wt, c0, c1)
+    assert torch.equal(ss, ss2) and torch.equal(out, out2)
+
+
+@pytest.mark.parametrize("M", [1, 300, 4096])
+def test_linear_rowscale_is_rms_norm_then_projection(dsk, M):
+    """kv_b on the raw latent with the RMS row scale in its epilogue against the
+    reference order of operations (mla.py:338-346: RMSNorm with weight w, then
+    kv_b) in fp32 on the same bf16 inputs: within the bf16 bar. The latent is a
+    strided view (row pitch 576 inside the kv_a output), the statistics come from
+    linear_rowsq, and the norm weight is folded into kv_b's input columns."""
+    from ds_kernels import mla as dm
+    g = torch.Generator().manual_seed(M + 9)
+    K, Hq = 2048, 3072
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(DEV)
+    w_qkva = (torch.randn(Hq + 576, K, generator=g) * 0.02).to(torch.bfloat16)
+    kvb = (torch.randn(4096, 512, generator=g) * 0.02).to(torch.bfloat16)
+    nw = 1.0 + 0.1 * torch.randn(512, generator=g)   # a non-trivial norm weight
+    y, ss = dsk.linear_rowsq(x, dsk.tile_weights(w_qkva[None])[0].to(DEV), Hq, Hq + 512)
+    lat = y[:, Hq:Hq + 512]                            # strided view, pitch 3648
+    kvb_w = dsk.tile_weights((kvb.float() * nw[None, :]).to(torch.bfloat16)[None])[0].to(DEV)
+    out = dsk.linear_rowscale(lat, kvb_w, ss, 512, 1e-6)
+    l32 = lat.float().cpu()
+    normed = l32 * torch.rsqrt((l32 * l32).mean(-1, keepdim=True) + 1e-6) * nw[None, :]
+    ref = normed @ kvb.float().T
+    assert out.shape == (M, 4096)
+    assert max_rel_err(np32(out), ref.numpy()) <= BF16_TOL
+    # and against this library's unfused pair (rms_norm kernel, then kv_upproj)
+    sep = dsk.kv_upproj(dsk.rms_norm(lat, nw.to(DEV)), dsk.tile_weights(kvb[None])[0].to(DEV))
+    assert max_rel_err(np32(out), np32(sep)) <= BF16_TOL
+    assert torch.equal(out, dsk.linear_rowscale(lat, kvb_w, ss, 512, 1e-6))
+
+
+def test_mla_projections_fused_norm_matches_separate_pass(mla_setup):
+    """The projection block with the latent norm in the epilogues against the
+    same block with the norm as its own pass (MLAWeights without the folded
+    kv_b weight): q and k_rot bit-identical, k_nope and v within the bf16 bar."""
+    import dataclasses
+    dm, w, W, wn = mla_setup
+    assert W.kvb_w is not None
+    b, s = 2, 256
+    g = torch.Generator().manual_seed(17)
+    x = torch.randn(b, s, 2048, generator=g).to(torch.bfloat16).to(DEV)
+    cos, sin = dm.yarn_cos_sin(s, device=torch.device(DEV))
+    fused = dm.mla_projections(x, W, cos, sin, with_latent=False)
+    sep = dm.mla_projections(x, dataclasses.replace(W, kvb_w=None), cos, sin)
+    assert fused[5] is None
+    for i in (0, 1, 4):
+        assert torch.equal(fused[i], sep[i])
+    for i in (2, 3):
+        assert max_rel_err(np32(fused[i]), np32(sep[i])) <= BF16_TOL
+
+
 def _softmax_ref(sc: torch.Tensor, scale: float, causal: bool) -> torch.Tensor:
     """CPU fp32 restatement of mla.py:366-381 on the same bf16 scores: scores *
     scale rounded to bf16, causal mask (query i of the last q_len positions sees
