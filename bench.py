@@ -273,27 +273,47 @@ def bench_mla(dsk, syn, torch, ev, reps=20, warmup=5):
 
 def bench_latent_decode(dsk, torch, dm, W, timed, dev, g):
     """Decode over the latent KV cache: the attention op alone (reads every
-    cached 1152-byte row once; HBM-bound) at a few (batch, cache length)
-    points, and one whole decode step (projections, cache append, absorbed
-    attention, W_UV, o_proj) for one new token after 4095 cached ones, beside
-    the full-sequence recompute at 4096 that a cache-less forward pays."""
+    cached token's latent and rotated RoPE key, 1152 bytes, once; HBM-bound) at
+    a few (batch, cache length) points, and one whole decode step (projections,
+    cache append, absorbed attention, W_UV, o_proj) for one new token after
+    4095 cached ones, beside the full-sequence recompute at 4096 that a
+    cache-less forward pays. The op is timed over enough copies of the cache
+    (at least 512 MB, cycled in order) that no call finds its rows in the
+    256 MB Infinity Cache, as a layer of a real model would not; each call
+    rotates its n new keys itself (rope_len = L - n), as in a decode step."""
+    from ds_kernels import ops
     A = dsk.AbsorbedMLAWeights.from_mla(W)
     cos, sin = dm.yarn_cos_sin(8192, device=dev)
     cos, sin = cos.to(torch.bfloat16), sin.to(torch.bfloat16)
     gbs = lambda nbytes, ms: nbytes / (ms * 1e-3) / 1e9  # noqa: E731
     res = {"attention_op": []}
     for b, L, n in ((1, 4096, 1), (4, 4096, 1), (16, 4096, 1), (1, 4096, 8)):
-        rows = torch.randn(b, L, 576, generator=g).to(torch.bfloat16).to(dev)
+        raw = torch.randn(b, L, 576, generator=g).to(torch.bfloat16).to(dev)
+        rows = torch.zeros(b, L, 640, dtype=torch.bfloat16, device=dev)   # LatentKVCache rows
+        rows[..., :576] = raw
+        c = cos[:L][None, None].expand(b, 1, L, 64)
+        sn = sin[:L][None, None].expand(b, 1, L, 64)
+        rows[..., 576:] = ops.rope_single(raw[:, None, :, 512:], c, sn)[:, 0]
+        copies = max(2, min(64, -(-(512 << 20) // (rows.numel() * 2))))
+        bufs = [rows] + [rows.clone() for _ in range(copies - 1)]
         q_abs = (torch.randn(b * n, 16, 512, generator=g) * 0.05).to(torch.bfloat16).to(dev)
         q_pe = torch.randn(b * n, 16, 64, generator=g).to(torch.bfloat16).to(dev)
         o = torch.empty(b * n, 16, 512, dtype=torch.bfloat16, device=dev)
-        t = timed(lambda: dsk.mla_decode_attention(q_abs, q_pe, rows[..., :512], rows[..., 512:],
-                                                   cos, sin, W.softmax_scale, out=o))
-        nbytes = b * L * 576 * 2 + 2 * b * n * 16 * (512 + 64 + 512) + 2 * L * 64 * 2
+        nxt = [0]
+
+        def call():
+            r = bufs[nxt[0] % copies]
+            nxt[0] += 1
+            dsk.mla_decode_attention(q_abs, q_pe, r[..., :512], r[..., 512:576], cos, sin,
+                                     W.softmax_scale, out=o, k_rope=r[..., 576:],
+                                     rope_len=L - n)
+        t = timed(call, per_graph=copies)
+        nbytes = b * L * 576 * 2 + 2 * b * n * 16 * (512 + 64 + 512)
         res["attention_op"].append({"batch": b, "cache_len": L, "new_tokens": n, "us": t * 1e3,
                                     "algorithmic_bytes": nbytes, "GB/s": gbs(nbytes, t),
-                                    "frac_of_8TB/s": gbs(nbytes, t) / PEAK_HBM_GBS})
-        del rows, q_abs, q_pe, o
+                                    "frac_of_8TB/s": gbs(nbytes, t) / PEAK_HBM_GBS,
+                                    "cache_copies": copies})
+        del raw, rows, bufs, q_abs, q_pe, o
     L = 4096
     x = torch.randn(1, L, 2048, generator=g).to(torch.bfloat16).to(dev)
     cache = dsk.LatentKVCache.for_inference(1, max_seq=L, device=dev)

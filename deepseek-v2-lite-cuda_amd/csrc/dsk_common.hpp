@@ -51,6 +51,49 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 __device__ __forceinline__ float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
+// ------------------------------------------------------------------ RoPE --
+// RoPE of one raw pair (x0, x1) = (x[2k], x[2k+1]) (mla.py:196-205): the
+// reference maps it to outputs k and k + d/2,
+//   lo = out[k] = x0 cos[k] - x1 sin[k], hi = out[k + d/2] = x1 cos[k + d/2] + x0 sin[k + d/2].
+// Every kernel that rotates keys uses this one expression, so rotated keys
+// written by different kernels are bitwise equal.
+__device__ __forceinline__ void rope_pair(float x0, float x1, float c_lo, float c_hi, float s_lo,
+                                          float s_hi, float& lo, float& hi) {
+  lo = x0 * c_lo - x1 * s_lo;
+  hi = x1 * c_hi + x0 * s_hi;
+}
+
+// ------------------------------------------------- memory-counter helpers --
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+// s_waitcnt lgkmcnt(0): this wave's LDS (and scalar) accesses are done.
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// Workgroup barrier without the release/acquire fences of __syncthreads():
+// those would wait for every in-flight DMA (vmcnt(0)) and drain the ring. The
+// DMA completion this barrier publishes is waited for explicitly (wait_vmcnt)
+// by every wave before it arrives; the "memory" clobber keeps the compiler
+// from moving LDS accesses across the barrier.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// Global->LDS DMA of 16 bytes per lane (1 KB per wave to lds_addr) from
+// base + voff, as inline asm. The compiler's wait-count bookkeeping does not
+// model this LDS-writing load alongside ordinary register loads (with both in
+// flight it falls back to waiting for every outstanding load before each use);
+// hidden from it, the register loads keep exact counts, which can only be
+// stricter than needed since this DMA is not counted. The "memory" clobber
+// keeps every other memory access in program order around it; completion is
+// waited for explicitly (wait_vmcnt) before the data is read.
+__device__ __forceinline__ void dma_1kb(const char* base, uint32_t voff, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(base), "s"(lds_addr) : "memory", "m0");
+}
+
 // ----------------------------------------------------------- wave reductions --
 // DPP-based full-wave reductions (quad_perm / row mirrors inside a 16-lane row,
 // then row_bcast15 / row_bcast31 across rows); the result is read from lane 63

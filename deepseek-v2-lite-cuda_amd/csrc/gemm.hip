@@ -88,8 +88,6 @@ __device__ __forceinline__ float silu_f(float x) {
   return x * __builtin_amdgcn_rcpf(1.f + __expf(-x));
 }
 
-// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
-// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
 // Reads an accumulator register where it is used: the epilogue then moves
 // the accumulators to VGPRs a few at a time instead of all at once.
 __device__ __forceinline__ float acc_read(float a) {
@@ -98,11 +96,6 @@ __device__ __forceinline__ float acc_read(float a) {
   return v;
 }
 
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
-}
 
 // Wait until at most min(ahead, MAXA) * NL vector-memory ops are pending.
 template <int MAXA, int NL>
@@ -115,12 +108,6 @@ __device__ __forceinline__ void wait_stage_landed(int ahead) {
   }
 }
 
-// Workgroup barrier without the release/acquire fences of __syncthreads():
-// those would wait for every in-flight DMA (vmcnt(0)) and drain the ring. The
-// DMA completion this barrier publishes is waited for explicitly (wait_vmcnt)
-// by every wave before it arrives; the "memory" clobber keeps the compiler
-// from moving LDS accesses across the barrier.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 // Scheduling groups for one K step: NMFMA MFMAs with the NREAD fragment reads
 // of the next step placed two after each of the first MFMAs (masks: 0x008 MFMA,
@@ -593,18 +580,6 @@ constexpr int kWideRowTiles = (kLdsPerCU - kWideRingBytes - 4096) / (kWideBM * 4
 constexpr int kWideLdsBytes = kWideRingBytes + kWideRowTiles * kWideBM * 4;
 constexpr int kRowScaleParts = 2;  // sum-of-squares partials an RMS row scale adds up
 
-// Global->LDS DMA of 16 bytes per lane (1 KB per wave to lds_addr) from
-// base + voff, as inline asm. The compiler's wait-count bookkeeping does not
-// model this LDS-writing load alongside ordinary register loads (with both in
-// flight it falls back to waiting for every outstanding load before each use);
-// hidden from it, the register loads keep exact counts, which can only be
-// stricter than needed since this DMA is not counted. The "memory" clobber
-// keeps every other memory access in program order around it; completion is
-// waited for explicitly (wait_vmcnt) before the workgroup barrier.
-__device__ __forceinline__ void dma_1kb(const char* base, uint32_t voff, uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-               :: "v"(voff), "s"(base), "s"(lds_addr) : "memory", "m0");
-}
 
 template <bool SWIGLU, bool GATHER>
 __global__ __launch_bounds__(64 * kWideWaves, 1) void wide_gemm_kernel(GemmArgs p) {

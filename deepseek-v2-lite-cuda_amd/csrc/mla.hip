@@ -282,8 +282,7 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeTensor a, RopeTensor b, i
       const float c_hi = u ? bf16hi(ch[k >> 1]) : bf16lo(ch[k >> 1]);
       const float s_lo = u ? bf16hi(sl[k >> 1]) : bf16lo(sl[k >> 1]);
       const float s_hi = u ? bf16hi(sh[k >> 1]) : bf16lo(sh[k >> 1]);
-      lo[u] = x0 * c_lo - x1 * s_lo;
-      hi[u] = x1 * c_hi + x0 * s_hi;
+      rope_pair(x0, x1, c_lo, c_hi, s_lo, s_hi, lo[u], hi[u]);
     }
     olo[j >> 1] = pack_bf16x2(lo[0], lo[1]);
     ohi[j >> 1] = pack_bf16x2(hi[0], hi[1]);

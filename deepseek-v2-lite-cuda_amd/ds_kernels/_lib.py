@@ -46,8 +46,9 @@ SIGNATURES = {
     "dsk_linear_batched": (_I, [_P, _I64, _I64, _P, _P, _I64, _I64, _I, _I, _I, _I, _P]),
     "dsk_linear_split": (_I, [_P, _I64, _P, _P, _I64, _P, _I64, _I, _I, _I, _I, _P]),
     "dsk_mla_decode_workspace_size": (_SZ, [_I, _I, _I]),
-    "dsk_mla_decode_attention": (_I, [_P, _I64, _I64, _P, _I64, _I64, _P, _P, _I64, _I64, _P,
-                                      _P, _F, _F, _I, _I, _I, _P, _I64, _I64, _P, _SZ, _P]),
+    "dsk_mla_decode_attention": (_I, [_P, _I64, _I64, _P, _I64, _I64, _P, _P, _P, _I, _I64,
+                                      _I64, _P, _P, _F, _F, _I, _I, _I, _P, _I64, _I64, _P, _SZ,
+                                      _P]),
     "dsk_rms_norm": (_I, [_P, _I64, _P, _P, _I64, _I, _I, _F, _P]),
     "dsk_rms_norm_f32": (_I, [_P, _I64, _P, _P, _I64, _I, _I, _F, _P]),
     "dsk_rope": (_I, [_P, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _I, _I, _I, _I, _P]),

@@ -4,18 +4,20 @@ LatentKVCache mirrors src/kernels/mla_cache.py:29-219 (same constructor,
 properties, update/get/reset, errors and repr): per token it keeps the raw
 compressed latent (kv_lora_rank, before the RMSNorm) and the raw shared RoPE
 key (rope_head_dim, before RoPE), 576 bf16 values instead of the 5120 of the
-up-projected K and V. Both live in one [bsz, max_seq, 576] buffer, the layout
-kv_a_proj_with_mqa produces, so one cache row is one contiguous 1152-byte read
-for the attention kernel; `kv_latent` and `k_pe_cache` are views of it with the
-reference's shapes.
+up-projected K and V. Both live in one [bsz, max_seq, 640] buffer, in the
+layout kv_a_proj_with_mqa produces, followed by the RoPE key after RoPE
+(`k_rope`, 64 more values per token, written once per token by the first
+attention that reads it): the attention kernel reads the latent and the rotated
+key of a token (1152 bytes) and no angle tables. `kv_latent` and `k_pe_cache`
+are views with the reference's shapes.
 
 mla_decode_forward runs DeepSeekMLA.forward (src/reference/mla.py:295-393) for
 new tokens against the cache in the absorbed form: the kv_b up-projection is
 folded into the query (q_abs = (W_UK * w)^T q_nope per head) and into the
 output ((W_UV * w) o_lat per head), and `ops.mla_decode_attention` attends
 straight over the cached raw latents, computing each key's RMS scale and RoPE
-on the fly. The reference itself has no attention over its cache (mla.py:7
-recomputes K and V for the whole sequence).
+on the fly and rotating each cached key once. The reference itself has no
+attention over its cache (mla.py:7 recomputes K and V for the whole sequence).
 """
 from __future__ import annotations
 
@@ -34,6 +36,8 @@ class LatentKVCache:
 
     kv_latent  [bsz, max_seq, kv_lora_rank]   raw latent (pre-norm), a view
     k_pe_cache [bsz, max_seq, rope_head_dim]  raw shared RoPE key, a view
+    k_rope     [bsz, max_seq, rope_head_dim]  the RoPE key after RoPE (positions
+                                              < rope_len hold it), a view
     """
 
     def __init__(self, bsz: int, max_seq: int, kv_lora_rank: int = 512, rope_head_dim: int = 64,
@@ -49,10 +53,13 @@ class LatentKVCache:
         self.device = torch.device(device)
         self.dtype = dtype
         self._len = 0
-        self.rows = torch.zeros((bsz, max_seq, kv_lora_rank + rope_head_dim), dtype=dtype,
+        self._rope_len = 0   # leading positions whose k_rope is valid
+        w = kv_lora_rank + rope_head_dim
+        self.rows = torch.zeros((bsz, max_seq, w + rope_head_dim), dtype=dtype,
                                 device=self.device)
         self.kv_latent = self.rows[..., :kv_lora_rank]
-        self.k_pe_cache = self.rows[..., kv_lora_rank:]
+        self.k_pe_cache = self.rows[..., kv_lora_rank:w]
+        self.k_rope = self.rows[..., w:]
 
     @property
     def current_len(self) -> int:
@@ -65,8 +72,14 @@ class LatentKVCache:
         return self.max_seq - self._len
 
     @property
+    def rope_len(self) -> int:
+        """Leading positions whose rotated key (k_rope) is valid."""
+        return min(self._rope_len, self._len)
+
+    @property
     def memory_bytes(self) -> int:
-        """Bytes held by the latent and RoPE-key planes (mla_cache.py:92-98)."""
+        """Bytes held by the latent and RoPE-key planes (mla_cache.py:92-98); the
+        rotated keys take rope_head_dim more values per token beside them."""
         return (self.kv_latent.numel() + self.k_pe_cache.numel()) * self.rows.element_size()
 
     def update(self, compressed_kv: torch.Tensor, k_pe: torch.Tensor) -> None:
@@ -85,6 +98,7 @@ class LatentKVCache:
             raise RuntimeError(f"KV cache overflow: current_len={self._len}, new_tokens={n}, "
                                f"max_seq={self.max_seq}. Increase max_seq or reset the cache.")
         slot = slice(self._len, self._len + n)
+        self._rope_len = self.rope_len   # rows from _len on are rewritten
         self.kv_latent[:, slot, :] = compressed_kv.to(self.device, self.dtype)
         self.k_pe_cache[:, slot, :] = k_pe.to(self.device, self.dtype)
         self._len += n
@@ -97,7 +111,8 @@ class LatentKVCache:
         if self._len + n > self.max_seq:
             raise RuntimeError(f"KV cache overflow: current_len={self._len}, new_tokens={n}, "
                                f"max_seq={self.max_seq}. Increase max_seq or reset the cache.")
-        rows = self.rows[:, self._len:self._len + n]
+        self._rope_len = self.rope_len   # rows from _len on are rewritten
+        rows = self.rows[:, self._len:self._len + n, :self.kv_lora_rank + self.rope_head_dim]
         self._len += n
         return rows
 
@@ -113,6 +128,7 @@ class LatentKVCache:
     def reset(self) -> None:
         """Start a new sequence; keeps the buffers (mla_cache.py:171-176)."""
         self._len = 0
+        self._rope_len = 0
 
     def __repr__(self) -> str:
         used = (self._len * (self.kv_lora_rank + self.rope_head_dim) * self.rows.element_size()
@@ -179,6 +195,8 @@ def _attend_up_projected(q: torch.Tensor, cache: LatentKVCache, W: MLAWeights, c
     sk = sin[:L][None, None].expand(b, 1, L, r)
     q_rot = ops.rope_single(q[..., nope:].transpose(1, 2), cq, sq)        # [b, h, n, r]
     k_rot = ops.rope_single(pe[:, None], ck, sk)                          # [b, 1, L, r]
+    cache.k_rope[:, :L].copy_(k_rot[:, 0])       # every cached key rotated once
+    cache._rope_len = L
     qf = torch.cat([q[..., :nope].transpose(1, 2), q_rot], dim=-1)       # [b, h, n, 192]
     kf = torch.cat([kv[..., :nope], k_rot.expand(b, h, L, r)], dim=-1)   # [b, h, L, 192]
     scores = torch.matmul(qf, kf.transpose(-1, -2).contiguous())         # bf16 [b, h, n, L]
@@ -257,7 +275,9 @@ def _decode_step(x: torch.Tensor, W: MLAWeights, cache: LatentKVCache, rows: tor
         q_abs = torch.bmm(q[..., :nope].transpose(0, 1).contiguous(), A.w_uk)
     o_lat = torch.empty((h, T, lora), dtype=torch.bfloat16, device=x.device)
     ops.mla_decode_attention(q_abs.transpose(0, 1), q[..., nope:], latent, k_pe, cos, sin,
-                             W.softmax_scale, eps, out=o_lat.transpose(0, 1))
+                             W.softmax_scale, eps, out=o_lat.transpose(0, 1),
+                             k_rope=cache.k_rope[:, :L], rope_len=cache.rope_len)
+    cache._rope_len = L          # the kernel rotated and stored the new keys
     if small:   # o[t, h*v:(h+1)*v] = o_lat[h, t] @ (W_UV[h] * w)^T, written token-major
         o = torch.empty((T, h * vd), dtype=torch.bfloat16, device=x.device)
         ops.linear_batched(o_lat, A.uv_tiled, out=o.view(T, h, vd).transpose(0, 1))

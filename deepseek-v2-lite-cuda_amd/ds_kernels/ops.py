@@ -524,16 +524,20 @@ def attn_softmax_(scores: torch.Tensor, scale: float, causal: bool = True) -> to
 
 def mla_decode_attention(q_abs: torch.Tensor, q_pe: torch.Tensor, latent: torch.Tensor,
                          k_pe: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, scale: float,
-                         eps: float = 1e-6, out: torch.Tensor = None) -> torch.Tensor:
+                         eps: float = 1e-6, out: torch.Tensor = None,
+                         k_rope: torch.Tensor = None, rope_len: int = 0) -> torch.Tensor:
     """Absorbed MLA attention of T = bsz * n new tokens over the raw latent
     cache (the attention of mla.py:356-384 on cached tokens, latent RMSNorm
-    and RoPE applied on the fly).
+    applied on the fly).
     q_abs: bf16 [T, 16, 512] ((W_UK * w)^T q_nope per head); q_pe: bf16
     [T, 16, 64], raw (pre-RoPE); latent / k_pe: bf16 [bsz, L, 512] / [bsz, L, 64]
     cache views sharing their batch and token strides, the last n tokens being
-    the new ones; cos/sin: bf16 [>= L, 64] by position. All may be strided
-    views with a contiguous last dim. Returns bf16 [T, 16, 512] (into `out` if
-    given): sum_j softmax_j r_j x_j per head."""
+    the new ones; cos/sin: bf16 [>= L, 64] by position. k_rope: bf16
+    [bsz, L, 64] with the same strides, the keys after RoPE: rows < rope_len
+    are read, rows from rope_len on are rotated from k_pe and written (None: a
+    scratch buffer, every key rotated here). All may be strided views with a
+    contiguous last dim. Returns bf16 [T, 16, 512] (into `out` if given):
+    sum_j softmax_j r_j x_j per head."""
     op = "mla_decode_attention"
     for t, nm in ((q_abs, "q_abs"), (q_pe, "q_pe"), (latent, "latent"), (k_pe, "k_pe"),
                   (cos, "cos"), (sin, "sin")):
@@ -548,6 +552,16 @@ def mla_decode_attention(q_abs: torch.Tensor, q_pe: torch.Tensor, latent: torch.
     _req(k_pe.shape == (b, L, 64), f"{op}: k_pe must be [bsz, L, 64].")
     _req(latent.stride()[:2] == k_pe.stride()[:2],
          f"{op}: latent and k_pe must share batch and token strides.")
+    if k_rope is None:
+        rows = torch.empty((b, L, 640), dtype=torch.bfloat16, device=latent.device)
+        rows[..., :512].copy_(latent)
+        rows[..., 512:576].copy_(k_pe)
+        latent, k_pe, k_rope, rope_len = rows[..., :512], rows[..., 512:576], rows[..., 576:], 0
+    _req(isinstance(k_rope, torch.Tensor) and k_rope.is_cuda and k_rope.dtype == torch.bfloat16
+         and k_rope.shape == (b, L, 64) and k_rope.stride()[:2] == latent.stride()[:2]
+         and k_rope.stride(-1) == 1,
+         f"{op}: k_rope must be bf16 [bsz, L, 64] with the strides of latent.")
+    _req(isinstance(rope_len, int) and 0 <= rope_len <= L, f"{op}: need 0 <= rope_len <= {L}.")
     _req(b > 0 and T % b == 0, f"{op}: T={T} is not a multiple of bsz={b}.")
     n = T // b
     _req(n <= L, f"{op}: {n} new tokens but only {L} in the cache.")
@@ -565,9 +579,9 @@ def mla_decode_attention(q_abs: torch.Tensor, q_pe: torch.Tensor, latent: torch.
     with torch.cuda.device(q_abs.device):
         check(lib.dsk_mla_decode_attention(
             q_abs.data_ptr(), q_abs.stride(0), q_abs.stride(1), q_pe.data_ptr(), q_pe.stride(0),
-            q_pe.stride(1), latent.data_ptr(), k_pe.data_ptr(), latent.stride(1), ld_batch,
-            cos.data_ptr(), sin.data_ptr(), float(eps), float(scale), b, n, L, out.data_ptr(),
-            out.stride(0), out.stride(1), ws.data_ptr(), ws.numel(),
+            q_pe.stride(1), latent.data_ptr(), k_pe.data_ptr(), k_rope.data_ptr(), rope_len,
+            latent.stride(1), ld_batch, cos.data_ptr(), sin.data_ptr(), float(eps), float(scale),
+            b, n, L, out.data_ptr(), out.stride(0), out.stride(1), ws.data_ptr(), ws.numel(),
             stream_handle(q_abs.device)), op)
     return out
 

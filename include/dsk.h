@@ -299,19 +299,24 @@ int dsk_attn_softmax(dsk_bf16* scores, int64_t ld, int64_t rows, int kv_len,
  *   o[t,h]  = sum_j softmax(s)_j r_j x_j        (fp32, stored as bf16)
  * with r_j = rsqrt(mean(x_j^2) + eps) and rope as in dsk_rope (angles of the
  * row's position in cos/sin [positions, 64], which must cover kv_len rows).
- * q_abs[t,h] (512) is (W_UK[h] * norm_weight)^T q_nope[t,h]; the caller
- * applies (W_UV[h] * norm_weight) and o_proj to o. Element strides: q_abs at
- * t * qa_tok + h * qa_head, q_pe (raw, pre-RoPE) at t * qp_tok + h * qp_head,
- * cache token j of sequence b at b * ld_batch + j * ld_tok in latent and in
- * k_pe (the two may interleave in one 576-wide row), o at t * o_tok +
- * h * o_head. This is the attention of DeepSeekMLA.forward (mla.py:318-384)
- * over the cached prefix plus the new tokens; the reference has no kernel for
- * it (it recomputes K and V for the whole sequence). */
+ * k_rope holds rope(k_pe_j), the rotated keys in dsk_rope's output layout:
+ * rows j < rope_len are read from it; rows rope_len <= j < kv_len are rotated
+ * here from k_pe and written to it (each key is rotated once, by the call
+ * after its append). q_abs[t,h] (512) is (W_UK[h] * norm_weight)^T
+ * q_nope[t,h]; the caller applies (W_UV[h] * norm_weight) and o_proj to o.
+ * Element strides: q_abs at t * qa_tok + h * qa_head, q_pe (raw, pre-RoPE) at
+ * t * qp_tok + h * qp_head, cache token j of sequence b at b * ld_batch +
+ * j * ld_tok in latent, k_pe and k_rope (the three may interleave in one row,
+ * LatentKVCache's 640-wide rows), o at t * o_tok + h * o_head. This is the
+ * attention of DeepSeekMLA.forward (mla.py:318-384) over the cached prefix
+ * plus the new tokens; the reference has no kernel for it (it recomputes K and
+ * V for the whole sequence). */
 size_t dsk_mla_decode_workspace_size(int batch, int q_len, int kv_len);
 int dsk_mla_decode_attention(const dsk_bf16* q_abs, int64_t qa_tok,
                              int64_t qa_head, const dsk_bf16* q_pe,
                              int64_t qp_tok, int64_t qp_head,
                              const dsk_bf16* latent, const dsk_bf16* k_pe,
+                             dsk_bf16* k_rope, int rope_len,
                              int64_t ld_tok, int64_t ld_batch,
                              const dsk_bf16* cos_tab, const dsk_bf16* sin_tab,
                              float eps, float scale, int batch, int q_len,

@@ -146,24 +146,30 @@ def test_mla_decode_validation(dsk):
     assert ws == 64 * (16 * 512 + 32) * 4
     assert lib.dsk_mla_decode_workspace_size(2, 3, 65) == 2 * 3 * 2 * (16 * 512 + 32) * 4
     assert lib.dsk_mla_decode_workspace_size(1, 600, 4096) == 256  # one split per token: no partials
-    # argument order: q_abs, qa_tok, qa_head, q_pe, qp_tok, qp_head, latent, k_pe, ld_tok,
-    # ld_batch, cos, sin, eps, scale, batch, q_len, kv_len, out, o_tok, o_head, ws, bytes, stream
-    def call(q_len=1, kv_len=64, ld_tok=576, ld_batch=576 * 64, batch=1, qa=(8192, 512),
-             out=16, bytes_=1 << 30, q_abs=16):
-        return lib.dsk_mla_decode_attention(q_abs, qa[0], qa[1], 16, 3072, 192, 16, 16, ld_tok,
-                                            ld_batch, 16, 16, 1e-6, 0.1, batch, q_len, kv_len,
-                                            out, 8192, 512, 16, bytes_, None)
-    assert lib.dsk_mla_decode_attention(None, 0, 0, None, 0, 0, None, None, 0, 0, None, None,
-                                        1e-6, 0.1, 0, 1, 64, None, 0, 0, None, 0, None) == 0
+    # argument order: q_abs, qa_tok, qa_head, q_pe, qp_tok, qp_head, latent, k_pe, k_rope,
+    # rope_len, ld_tok, ld_batch, cos, sin, eps, scale, batch, q_len, kv_len, out, o_tok,
+    # o_head, ws, bytes, stream
+    def call(q_len=1, kv_len=64, ld_tok=640, ld_batch=640 * 64, batch=1, qa=(8192, 512),
+             out=16, bytes_=1 << 30, q_abs=16, k_rope=16, rope_len=0):
+        return lib.dsk_mla_decode_attention(q_abs, qa[0], qa[1], 16, 3072, 192, 16, 16, k_rope,
+                                            rope_len, ld_tok, ld_batch, 16, 16, 1e-6, 0.1, batch,
+                                            q_len, kv_len, out, 8192, 512, 16, bytes_, None)
+    assert lib.dsk_mla_decode_attention(None, 0, 0, None, 0, 0, None, None, None, 0, 0, 0, None,
+                                        None, 1e-6, 0.1, 0, 1, 64, None, 0, 0, None, 0, None) == 0
+    assert call(rope_len=65) == 1 and "rope_len" in _err(dsk)
+    assert call(rope_len=-1) == 1 and "rope_len" in _err(dsk)
+    assert call(k_rope=None) == 2
+    assert call(k_rope=24) == 3
+    assert call(kv_len=1 << 21, ld_batch=640 << 21) == 1 and "2 GiB" in _err(dsk)
     assert call(q_len=65) == 1 and "q_len <= kv_len" in _err(dsk)
     assert call(ld_tok=60) == 1 and "token stride" in _err(dsk)
-    assert call(batch=2, ld_batch=576 * 63) == 1 and "batch" in _err(dsk)
+    assert call(batch=2, ld_batch=640 * 63) == 1 and "batch" in _err(dsk)
     assert call(qa=(8192, 500)) == 3 and "multiples of 8" in _err(dsk)
     assert call(q_abs=None) == 2
     assert call(q_abs=24) == 3
     assert call(out=18) == 3
     assert call(kv_len=4096, bytes_=1024) == 5 and "workspace" in _err(dsk)
-    assert call(batch=256, q_len=256, kv_len=256, ld_batch=576 * 256) == 1 and "65535" in _err(dsk)
+    assert call(batch=256, q_len=256, kv_len=256, ld_batch=640 * 256) == 1 and "65535" in _err(dsk)
 
 
 def test_linear_batched_validation(dsk):

@@ -87,27 +87,84 @@ def test_cache_holds_raw_projection_rows(setup):
     assert max_rel_err(np32(pe), kva[..., 512:]) <= BF16_TOL
 
 
-def test_decode_attention_op_strided_inputs(setup):
-    """The op on a separately allocated, non-interleaved cache (latent and k_pe
-    in their own tensors with equal strides) and a strided output view gives the
-    same result as on the cache's interleaved rows."""
+def _rotated_rows(dsk, rows, cos, sin):
+    """[b, L, 640] cache rows from raw [b, L, 576] ones: the RoPE key after
+    dsk_rope (the prompt path's rotation) in columns 576..639."""
+    b, L, _ = rows.shape
+    out = torch.zeros(b, L, 640, dtype=torch.bfloat16, device=DEV)
+    out[..., :576] = rows
+    c = cos[:L][None, None].expand(b, 1, L, 64)
+    s = sin[:L][None, None].expand(b, 1, L, 64)
+    from ds_kernels import ops
+    out[..., 576:] = ops.rope_single(rows[:, None, :, 512:], c, s)[:, 0]
+    return out
+
+
+def test_decode_attention_op_rotated_keys(setup):
+    """The op over cached rotated keys (rope_len = L), over none (rope_len = 0:
+    every key rotated in the kernel from k_pe and stored), over the last few
+    (rope_len = L - 5, a decode step) and on separately allocated planes with
+    equal strides and a strided output: all give the same bits, the kernel's
+    rotation equals dsk_rope's bit for bit, and rows below rope_len are not
+    written."""
     dsk, W, A, wn, cos, sin = setup
     g = torch.Generator().manual_seed(9)
     b, n, L = 2, 3, 150
-    rows = torch.randn(b, L, 576, generator=g).to(torch.bfloat16).to(DEV)
+    raw = torch.randn(b, L, 576, generator=g).to(torch.bfloat16).to(DEV)
     q_abs = (torch.randn(b * n, 16, 512, generator=g) * 0.1).to(torch.bfloat16).to(DEV)
     q_pe = torch.randn(b * n, 16, 64, generator=g).to(torch.bfloat16).to(DEV)
     scale = W.softmax_scale
-    a = dsk.mla_decode_attention(q_abs, q_pe, rows[..., :512], rows[..., 512:], cos, sin, scale)
+    rows = _rotated_rows(dsk, raw, cos, sin)
+    krot = rows[..., 576:].clone()
+
+    def run(rows_, rope_len, out=None):
+        return dsk.mla_decode_attention(q_abs, q_pe, rows_[..., :512], rows_[..., 512:576], cos,
+                                        sin, scale, out=out, k_rope=rows_[..., 576:640],
+                                        rope_len=rope_len)
+    a = run(rows, L)
+    fresh = rows.clone()
+    fresh[..., 576:] = 0
+    b0 = run(fresh, 0)
+    part = rows.clone()
+    part[:, L - 5:, 576:] = 0
+    b5 = run(part, L - 5)
+    torch.cuda.synchronize()
+    assert torch.equal(b0.cpu(), a.cpu()) and torch.equal(b5.cpu(), a.cpu())
+    assert torch.equal(fresh[..., 576:].cpu(), krot.cpu())
+    assert torch.equal(part[..., 576:].cpu(), krot.cpu())
+    # separate planes (row pitch 576 in each) and a strided output view
     lat = torch.zeros(b, L, 576, dtype=torch.bfloat16, device=DEV)
     pe = torch.zeros(b, L, 576, dtype=torch.bfloat16, device=DEV)
-    lat[..., :512] = rows[..., :512]
-    pe[..., :64] = rows[..., 512:]
+    kr = torch.zeros(b, L, 576, dtype=torch.bfloat16, device=DEV)
+    lat[..., :512] = raw[..., :512]
+    pe[..., :64] = raw[..., 512:]
+    kr[..., :64] = krot
     out = torch.zeros(16, b * n, 512, dtype=torch.bfloat16, device=DEV)
     dsk.mla_decode_attention(q_abs, q_pe, lat[..., :512], pe[..., :64], cos, sin, scale,
-                             out=out.transpose(0, 1))
+                             out=out.transpose(0, 1), k_rope=kr[..., :64], rope_len=L)
+    # without k_rope the op rotates every key into a scratch buffer
+    c = dsk.mla_decode_attention(q_abs, q_pe, raw[..., :512], raw[..., 512:], cos, sin, scale)
     torch.cuda.synchronize()
-    assert torch.equal(out.transpose(0, 1).cpu(), a.cpu())
+    assert torch.equal(out.transpose(0, 1).cpu(), a.cpu()) and torch.equal(c.cpu(), a.cpu())
+
+
+def test_decode_after_reference_update(setup):
+    """A cache filled through the reference API (update() with raw rows, nothing
+    rotated) and then a decode step: the kernel rotates the whole prefix, and the
+    new token's output matches the full-sequence oracle."""
+    dsk, W, A, wn, cos, sin = setup
+    g = torch.Generator().manual_seed(21)
+    b, S = 2, 200
+    x = torch.randn(b, S, 2048, generator=g).to(torch.bfloat16)
+    kva = torch.from_numpy(ol.linear(np32(x[:, :S - 1]), wn["kva"])).to(torch.bfloat16)
+    cache = dsk.LatentKVCache(b, S, device=DEV)
+    cache.update(kva[..., :512], kva[..., 512:])
+    assert cache.rope_len == 0
+    out = dsk.mla_decode_forward(x[:, S - 1:].to(DEV), W, cache, cos, sin, A)
+    torch.cuda.synchronize()
+    assert cache.rope_len == S
+    ref = _oracle(x, wn)[:, S - 1:]
+    assert max_rel_err(np32(out), ref) <= BF16_TOL
 
 
 def test_decode_op_rejects_bad_shapes(setup):

@@ -37,9 +37,12 @@ def test_update_get_round_trip_and_views():
     assert torch.equal(lat, lat1) and torch.equal(pe, pe1)
     # zero-copy views of the cache buffers
     assert lat.data_ptr() == c.kv_latent.data_ptr() and pe.data_ptr() == c.k_pe_cache.data_ptr()
-    # one 576-wide row per token: latent then RoPE key, as kv_a_proj_with_mqa emits them
+    # one row per token: latent then RoPE key, as kv_a_proj_with_mqa emits them,
+    # then the rotated key (written by the first attention over the token)
+    assert c.rows.shape == (2, 10, 640)
     assert torch.equal(c.rows[:, :7, :512], c.get()[0])
-    assert torch.equal(c.rows[:, 3:7, 512:], pe2)
+    assert torch.equal(c.rows[:, 3:7, 512:576], pe2)
+    assert c.k_rope.shape == (2, 10, 64) and c.k_rope.data_ptr() == c.rows[..., 576:].data_ptr()
     assert c.get(0)[0].shape == (2, 0, 512)
 
 
@@ -97,6 +100,24 @@ def test_append_slots_reserves_views_in_order():
     with pytest.raises(RuntimeError, match="KV cache overflow: current_len=5, new_tokens=2"):
         c.append_slots(2)
     assert c.current_len == 5
+
+
+def test_rotated_key_count_follows_the_rows():
+    """rope_len counts the leading positions whose rotated key is valid: rows
+    rewritten by update / append_slots (after a rollback of the length, or a
+    reset) drop out of it."""
+    c = LatentKVCache(1, 8, device="cpu")
+    c.update(_tokens(1, 4, 0, 512), _tokens(1, 4, 1, 64))
+    assert c.rope_len == 0
+    c._rope_len = 4                      # as an attention over the 4 tokens leaves it
+    assert c.rope_len == 4
+    c.append_slots(2)
+    assert c.rope_len == 4 and c.current_len == 6
+    c._len = 3                           # roll back: row 3 will be rewritten
+    c.update(_tokens(1, 1, 2, 512), _tokens(1, 1, 3, 64))
+    assert c.rope_len == 3 and c.current_len == 4
+    c.reset()
+    assert c.rope_len == 0
 
 
 def test_rejected_decode_step_leaves_the_cache_length():
