@@ -71,8 +71,6 @@ __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
 }
-// s_waitcnt lgkmcnt(0): this wave's LDS (and scalar) accesses are done.
-__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
 // Workgroup barrier without the release/acquire fences of __syncthreads():
 // those would wait for every in-flight DMA (vmcnt(0)) and drain the ring. The
