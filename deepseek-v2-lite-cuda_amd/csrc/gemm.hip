@@ -977,8 +977,8 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void wide_gemm_kernel(GemmArgs 
 // parallelism rather than reuse:
 //   * one workgroup per (group, 64 weight rows): for SwiGLU the 32 gate rows
 //     and the matching 32 up rows of 32 output columns, otherwise 64
-//     consecutive rows; workgroups of empty groups exit at once, so idle
-//     experts cost no bandwidth;
+//     consecutive rows; the workgroups are handed to the non-empty groups in
+//     order and the rest exit at once, so idle experts cost no bandwidth;
 //   * the 4 waves split K four ways; each lane loads its MFMA fragments of
 //     weights and tokens straight from global memory into registers (no LDS,
 //     no barrier in the K loop), one batch of K steps ahead of the MFMAs, so
@@ -1006,12 +1006,38 @@ __global__ __launch_bounds__(kSkinnyThreads) void skinny_gemm_kernel(GemmArgs p,
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int g = blockIdx.x / n_blocks;
+  int g = blockIdx.x / n_blocks;
   const int nb = blockIdx.x - g * n_blocks;
   int mb = 0, me = p.M;
   if (p.offsets != nullptr) {
-    mb = min(max(p.offsets[g], 0), p.M);
-    me = min(max(p.offsets[g + 1], mb), p.M);
+    // The grid holds n_blocks workgroups per group, but only non-empty groups
+    // have work: workgroup ordinal g takes the g-th non-empty group. The busy
+    // workgroups thus come first in dispatch order, and the idle ones, all at
+    // the end of the grid, do not hold workgroup slots between them.
+    const int G = gridDim.x / n_blocks;
+    int ord = g;
+    g = -1;
+    for (int base = 0; base < G; base += 64) {
+      const int gi = base + lane;
+      int lo = 0, hi = 0;
+      if (gi < G) {
+        lo = min(max(p.offsets[gi], 0), p.M);
+        hi = min(max(p.offsets[gi + 1], lo), p.M);
+      }
+      const bool busy = hi > lo;
+      const uint64_t mask = __ballot(busy);
+      const int count = __popcll(mask);
+      if (ord < count) {  // uniform
+        const int rank = __popcll(mask & ((1ull << lane) - 1ull));
+        const int src = __ffsll((unsigned long long)__ballot(busy && rank == ord)) - 1;
+        g = base + src;
+        mb = __builtin_amdgcn_readfirstlane(__shfl(lo, src, 64));
+        me = __builtin_amdgcn_readfirstlane(__shfl(hi, src, 64));
+        break;
+      }
+      ord -= count;
+    }
+    if (g < 0) return;  // uniform: past the non-empty groups
   }
   if (mb >= me) return;  // uniform: empty group
 
