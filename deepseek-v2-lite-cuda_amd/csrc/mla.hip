@@ -437,6 +437,166 @@ extern "C" int dsk_rope(const dsk_bf16* x, int64_t sb, int64_t sh, int64_t ss,
                      0, S, d, stream);
 }
 
+// ----------------------------------------------- attention operand pack ---
+// The full-sequence attention of DeepSeekMLA.forward (mla.py:354-366) multiplies
+// query_states [b, h, s, 192] = (q_nope | rotated q_pe) by key_states^T, with
+// key_states = (k_nope | rotated k_pe, broadcast over the heads), and the
+// probabilities by value_states [b, h, s, 128]. The projections leave q, k_nope,
+// v and k_pe as slices of token rows, so the batched products need them packed
+// head-major first. One pass does it: Q (the nope part copied, the rope part
+// rotated), K^T (k_nope and the rotated k_pe transposed through the LDS, 64
+// positions per workgroup) and V. The rotation is the RoPE kernel's expression
+// (rope_pair on bf16 table values), so Q and K^T are bitwise those of the RoPE
+// kernel followed by the copies.
+constexpr int kPackPos = 64;  // positions per workgroup
+constexpr int kPackNope = 128, kPackRope = 64, kPackV = 128;
+constexpr int kPackQK = kPackNope + kPackRope;  // 192: one Q row, one K column
+constexpr int kPackChunks = kPackQK / 8;        // 16-byte chunks per K row in the tile
+constexpr int kPackThreads = 256;
+
+// 16-byte slot of chunk c of position p in the K tile. The chunk index is XORed
+// with the position's octet (it stays inside its aligned block of 8 chunks), so
+// the transposing reads, 8 octets x 8 dimension pairs per wave instruction,
+// touch each LDS bank at most twice.
+__device__ __forceinline__ int pack_slot(int p, int c) {
+  return p * kPackChunks + (c ^ ((p >> 3) & 7));
+}
+
+__global__ __launch_bounds__(kPackThreads) void attn_pack_kernel(
+    const uint16_t* __restrict__ q, int64_t ld_q, const uint16_t* __restrict__ kv,
+    int64_t ld_kv, const uint16_t* __restrict__ kpe, int64_t ld_kpe,
+    const uint16_t* __restrict__ cos_t, const uint16_t* __restrict__ sin_t, int64_t ld_cs,
+    uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_t, uint16_t* __restrict__ v_out,
+    int S, int heads) {
+  __shared__ u32x4_t tile[kPackPos * kPackChunks];  // K rows of the block, 24 KB
+  const int tid = threadIdx.x;
+  const int pos0 = blockIdx.x * kPackPos;
+  const int hh = blockIdx.y;
+  const int bi = blockIdx.z;
+  const int npos = min(kPackPos, S - pos0);
+  const int64_t bh = (int64_t)bi * heads + hh;
+  const int64_t row0 = (int64_t)bi * S + pos0;  // token row of the block's first position
+
+  // q nope -> Q, v -> V, k nope -> tile: 16 chunks per position each
+#pragma unroll
+  for (int r = 0; r < kPackPos * 16 / kPackThreads; ++r) {
+    const int it = tid + kPackThreads * r;
+    const int p = it >> 4, c = it & 15;
+    if (p < npos) {
+      const uint16_t* kvr = kv + (row0 + p) * ld_kv + hh * (kPackNope + kPackV);
+      const u32x4_t qn =
+          *reinterpret_cast<const u32x4_t*>(q + (row0 + p) * ld_q + hh * kPackQK + 8 * c);
+      const u32x4_t kn = *reinterpret_cast<const u32x4_t*>(kvr + 8 * c);
+      const u32x4_t vv = *reinterpret_cast<const u32x4_t*>(kvr + kPackNope + 8 * c);
+      *reinterpret_cast<u32x4_t*>(q_out + (bh * S + pos0 + p) * kPackQK + 8 * c) = qn;
+      *reinterpret_cast<u32x4_t*>(v_out + (bh * S + pos0 + p) * kPackV + 8 * c) = vv;
+      tile[pack_slot(p, c)] = kn;
+    }
+  }
+  // rotation, 8 pairs per item: q_pe into Q, k_pe into the tile
+#pragma unroll
+  for (int r = 0; r < 2 * kPackPos * 4 / kPackThreads; ++r) {
+    const int it = tid + kPackThreads * r;
+    const bool is_k = it >= kPackPos * 4;
+    const int i2 = is_k ? it - kPackPos * 4 : it;
+    const int p = i2 >> 2, c = i2 & 3;
+    if (p < npos) {
+      const uint16_t* x = is_k ? kpe + (row0 + p) * ld_kpe + 16 * c
+                               : q + (row0 + p) * ld_q + hh * kPackQK + kPackNope + 16 * c;
+      const uint16_t* ct = cos_t + (int64_t)(pos0 + p) * ld_cs + 8 * c;
+      const uint16_t* st = sin_t + (int64_t)(pos0 + p) * ld_cs + 8 * c;
+      const u32x4_t x0 = *reinterpret_cast<const u32x4_t*>(x);
+      const u32x4_t x1 = *reinterpret_cast<const u32x4_t*>(x + 8);
+      const u32x4_t cl = *reinterpret_cast<const u32x4_t*>(ct);
+      const u32x4_t ch = *reinterpret_cast<const u32x4_t*>(ct + kPackRope / 2);
+      const u32x4_t sl = *reinterpret_cast<const u32x4_t*>(st);
+      const u32x4_t sh = *reinterpret_cast<const u32x4_t*>(st + kPackRope / 2);
+      u32x4_t olo, ohi;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float lo[2], hi[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const uint32_t xw = (2 * j + u) < 4 ? x0[2 * j + u] : x1[2 * j + u - 4];
+          const float c_lo = u ? bf16hi(cl[j]) : bf16lo(cl[j]);
+          const float c_hi = u ? bf16hi(ch[j]) : bf16lo(ch[j]);
+          const float s_lo = u ? bf16hi(sl[j]) : bf16lo(sl[j]);
+          const float s_hi = u ? bf16hi(sh[j]) : bf16lo(sh[j]);
+          rope_pair(bf16lo(xw), bf16hi(xw), c_lo, c_hi, s_lo, s_hi, lo[u], hi[u]);
+        }
+        olo[j] = pack_bf16x2(lo[0], lo[1]);
+        ohi[j] = pack_bf16x2(hi[0], hi[1]);
+      }
+      if (is_k) {
+        tile[pack_slot(p, 16 + c)] = olo;  // dims 128 + 8c .. : outputs k = 8c ..
+        tile[pack_slot(p, 20 + c)] = ohi;  // dims 160 + 8c .. : outputs k + 32
+      } else {
+        uint16_t* qo = q_out + (bh * S + pos0 + p) * kPackQK + kPackNope + 8 * c;
+        *reinterpret_cast<u32x4_t*>(qo) = olo;
+        *reinterpret_cast<u32x4_t*>(qo + kPackRope / 2) = ohi;
+      }
+    }
+  }
+  __syncthreads();
+  // K^T: rows 2dp and 2dp + 1, 8 positions (octet po) per item; 8 consecutive
+  // lanes cover one 128-byte row segment of each
+  const uint32_t* tw = reinterpret_cast<const uint32_t*>(tile);
+  uint16_t* kt_bh = k_t + bh * kPackQK * S + pos0;
+#pragma unroll
+  for (int r = 0; r < (kPackQK / 2) * 8 / kPackThreads; ++r) {
+    const int it = tid + kPackThreads * r;
+    const int po = it & 7, dp = it >> 3;
+    if (8 * po < npos) {
+      uint32_t w[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) w[i] = tw[pack_slot(8 * po + i, dp >> 2) * 4 + (dp & 3)];
+      u32x4_t lo, hi;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        lo[k] = __builtin_amdgcn_perm(w[2 * k + 1], w[2 * k], 0x05040100u);
+        hi[k] = __builtin_amdgcn_perm(w[2 * k + 1], w[2 * k], 0x07060302u);
+      }
+      *reinterpret_cast<u32x4_t*>(kt_bh + (int64_t)(2 * dp) * S + 8 * po) = lo;
+      *reinterpret_cast<u32x4_t*>(kt_bh + (int64_t)(2 * dp + 1) * S + 8 * po) = hi;
+    }
+  }
+}
+
+extern "C" int dsk_mla_attn_pack(const dsk_bf16* q, int64_t ld_q, const dsk_bf16* kv,
+                                 int64_t ld_kv, const dsk_bf16* k_pe, int64_t ld_kpe,
+                                 const dsk_bf16* cos_t, const dsk_bf16* sin_t, int64_t ld_cs,
+                                 dsk_bf16* q_out, dsk_bf16* k_t, dsk_bf16* v_out, int batch,
+                                 int seq, int heads, int nope, int rope, int v_dim,
+                                 void* stream) {
+  DSK_REQUIRE(nope == kPackNope && rope == kPackRope && v_dim == kPackV, DSK_ERR_INVALID_ARG,
+              "attn_pack: head dims must be nope 128, rope 64, v 128");
+  DSK_REQUIRE(batch >= 0 && seq >= 0 && heads >= 0, DSK_ERR_INVALID_ARG,
+              "attn_pack: negative size");
+  if ((int64_t)batch * seq * heads == 0) return DSK_OK;
+  DSK_REQUIRE(seq % 8 == 0, DSK_ERR_INVALID_ARG, "attn_pack: seq must be a multiple of 8");
+  DSK_REQUIRE(batch <= 65535 && heads <= 65535, DSK_ERR_INVALID_ARG,
+              "attn_pack: batch and heads must be at most 65535");
+  DSK_REQUIRE(q && kv && k_pe && cos_t && sin_t && q_out && k_t && v_out, DSK_ERR_NULL_PTR,
+              "attn_pack: NULL pointer");
+  DSK_REQUIRE(aligned16(q) && aligned16(kv) && aligned16(k_pe) && aligned16(cos_t) &&
+                  aligned16(sin_t) && aligned16(q_out) && aligned16(k_t) && aligned16(v_out) &&
+                  ld_q % 8 == 0 && ld_kv % 8 == 0 && ld_kpe % 8 == 0 && ld_cs % 8 == 0,
+              DSK_ERR_ALIGNMENT, "attn_pack: rows must be 16-byte aligned");
+  DSK_REQUIRE(ld_q >= (int64_t)heads * kPackQK && ld_kv >= (int64_t)heads * (kPackNope + kPackV) &&
+                  ld_kpe >= kPackRope && ld_cs >= kPackRope,
+              DSK_ERR_INVALID_ARG, "attn_pack: row stride smaller than the row");
+  const dim3 grid((unsigned)((seq + kPackPos - 1) / kPackPos), (unsigned)heads, (unsigned)batch);
+  hipLaunchKernelGGL(attn_pack_kernel, grid, dim3(kPackThreads), 0, as_stream(stream),
+                     reinterpret_cast<const uint16_t*>(q), ld_q,
+                     reinterpret_cast<const uint16_t*>(kv), ld_kv,
+                     reinterpret_cast<const uint16_t*>(k_pe), ld_kpe,
+                     reinterpret_cast<const uint16_t*>(cos_t),
+                     reinterpret_cast<const uint16_t*>(sin_t), ld_cs,
+                     reinterpret_cast<uint16_t*>(q_out), reinterpret_cast<uint16_t*>(k_t),
+                     reinterpret_cast<uint16_t*>(v_out), seq, heads);
+  return check_launch("attn_pack_kernel");
+}
+
 extern "C" int dsk_attn_softmax(dsk_bf16* scores, int64_t ld, int64_t rows, int kv_len,
                                 int q_len, float scale, int causal, void* stream) {
   DSK_REQUIRE(rows >= 0 && kv_len > 0 && q_len > 0, DSK_ERR_INVALID_ARG,

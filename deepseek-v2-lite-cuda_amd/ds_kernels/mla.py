@@ -114,6 +114,33 @@ class MLAWeights:
 
 
 # ------------------------------------------------------------- projections --
+def _projection_rows(x: torch.Tensor, W: MLAWeights, eps: float, with_latent: bool):
+    """q_proj, kv_a_proj and kv_b_proj (mla.py:318-346) as token rows: q [b, s,
+    h*(nope+rope)], kv [b, s, h*(nope+v)], kva [b, s, kv_lora+rope] (column
+    slices of the projection outputs, no copies) and the normalised latent (None
+    unless with_latent or needed by the unfused path)."""
+    h, nope, r, lora = W.n_heads, W.nope, W.rope_dim, W.kv_lora
+    nq = h * (nope + r)
+    fused_norm = W.q_kva is not None and W.kvb_w is not None and nq % 256 == 0 and lora % 256 == 0
+    if fused_norm:
+        y, ss = ops.linear_rowsq(x, W.q_kva, nq, nq + lora)            # [b,s,3072+576], [2, b*s]
+        q, kva = y[..., :nq], y[..., nq:]
+    elif W.q_kva is not None:
+        # one GEMM for both projections (q_proj alone leaves no partial round of
+        # tiles for kv_a's 576 columns to fill); q and kva are column slices
+        y = ops.linear(x, W.q_kva)                                     # [b,s,3072+576]
+        q, kva = y[..., :nq], y[..., nq:]
+    else:
+        q, kva = ops.linear(x, W.q), ops.linear(x, W.kva)
+    if fused_norm:
+        kv = ops.linear_rowscale(kva[..., :lora], W.kvb_w, ss, lora, eps)
+        latent = ops.rms_norm(kva[..., :lora], W.kva_norm, eps) if with_latent else None
+    else:
+        latent = ops.rms_norm(kva[..., :lora], W.kva_norm, eps)        # strided rows, no copy
+        kv = ops.kv_upproj(latent, W.kvb)
+    return q, kv, kva, latent
+
+
 def mla_projections(x: torch.Tensor, W: MLAWeights, cos: torch.Tensor, sin: torch.Tensor,
                     eps: float = 1e-6, with_latent: bool = True):
     """The projection block of DeepSeekMLA.forward (mla.py:318-352, BASELINE
@@ -131,26 +158,9 @@ def mla_projections(x: torch.Tensor, W: MLAWeights, cos: torch.Tensor, sin: torc
     computed by the rms_norm kernel only if with_latent; otherwise it is None."""
     b, s, _ = x.shape
     h, nope, r, vd, lora = W.n_heads, W.nope, W.rope_dim, W.v_dim, W.kv_lora
-    nq = h * (nope + r)
-    fused_norm = W.q_kva is not None and W.kvb_w is not None and nq % 256 == 0 and lora % 256 == 0
-    if fused_norm:
-        y, ss = ops.linear_rowsq(x, W.q_kva, nq, nq + lora)            # [b,s,3072+576], [2, b*s]
-        q, kva = y[..., :nq], y[..., nq:]
-    elif W.q_kva is not None:
-        # one GEMM for both projections (q_proj alone leaves no partial round of
-        # tiles for kv_a's 576 columns to fill); q and kva are column slices
-        y = ops.linear(x, W.q_kva)                                     # [b,s,3072+576]
-        q, kva = y[..., :nq], y[..., nq:]
-    else:
-        q, kva = ops.linear(x, W.q), ops.linear(x, W.kva)
+    q, kv, kva, latent = _projection_rows(x, W, eps, with_latent)
     q = q.view(b, s, h, nope + r).transpose(1, 2)                      # [b,h,s,192] view
-    if fused_norm:
-        kv = ops.linear_rowscale(kva[..., :lora], W.kvb_w, ss, lora, eps)
-        kv = kv.view(b, s, h, nope + vd).transpose(1, 2)
-        latent = ops.rms_norm(kva[..., :lora], W.kva_norm, eps) if with_latent else None
-    else:
-        latent = ops.rms_norm(kva[..., :lora], W.kva_norm, eps)        # strided rows, no copy
-        kv = ops.kv_upproj(latent, W.kvb).view(b, s, h, nope + vd).transpose(1, 2)
+    kv = kv.view(b, s, h, nope + vd).transpose(1, 2)
     k_pe = kva[..., lora:].view(b, s, 1, r).transpose(1, 2)           # [b,1,s,64] view
     cb = cos.to(torch.bfloat16)[None, None].expand(b, 1, s, r)         # batch stride 0
     sb = sin.to(torch.bfloat16)[None, None].expand(b, 1, s, r)
@@ -166,18 +176,26 @@ def mla_forward(x: torch.Tensor, W: MLAWeights, cos: torch.Tensor, sin: torch.Te
     and .V in torch (right-hand operands made contiguous before the batched
     products), the scale, causal mask, fp32 softmax and bf16 rounding in one
     pass of attn_softmax_.
-    x: bf16 [b, s, H] -> bf16 [b, s, H]."""
+    x: bf16 [b, s, H] -> bf16 [b, s, H], with s a multiple of 8 (the 16-byte
+    rows of the score and K^T buffers)."""
     b, s, H = x.shape
-    q_nope, q_rot, k_nope, v, k_rot, _ = mla_projections(x, W, cos, sin, eps, with_latent=False)
     h, nope, r = W.n_heads, W.nope, W.rope_dim
-    q = torch.cat([q_nope, q_rot], dim=-1)                             # [b,h,s,192]
-    # K^T built in place, contiguous (one pass instead of a cat and a transposed copy)
-    kT = torch.empty((b, h, nope + r, s), dtype=torch.bfloat16, device=x.device)
-    kT[:, :, :nope].copy_(k_nope.transpose(-1, -2))
-    kT[:, :, nope:].copy_(k_rot.transpose(-1, -2).expand(b, h, r, s))
+    if (nope, r, W.v_dim) == (128, 64, 128):
+        # Q, K^T and V packed head-major in one pass from the projection rows
+        # (RoPE of q_pe and k_pe included); other head dims assemble them by copies
+        qr, kv, kva, _ = _projection_rows(x, W, eps, with_latent=False)
+        q, kT, v = ops.mla_attn_pack(qr, kv, kva[..., W.kv_lora:], cos[:s], sin[:s], heads=h)
+    else:
+        q_nope, q_rot, k_nope, v, k_rot, _ = mla_projections(x, W, cos, sin, eps,
+                                                             with_latent=False)
+        q = torch.cat([q_nope, q_rot], dim=-1)                         # [b,h,s,192]
+        kT = torch.empty((b, h, nope + r, s), dtype=torch.bfloat16, device=x.device)
+        kT[:, :, :nope].copy_(k_nope.transpose(-1, -2))
+        kT[:, :, nope:].copy_(k_rot.transpose(-1, -2).expand(b, h, r, s))
+        v = v.contiguous()
     scores = torch.matmul(q, kT)                                       # bf16 [b,h,s,s]
     p = ops.attn_softmax_(scores, W.softmax_scale, causal=True)       # scale, mask, softmax
-    o = torch.matmul(p, v.contiguous())                                # [b,h,s,v]
+    o = torch.matmul(p, v)                                             # [b,h,s,v]
     o = o.transpose(1, 2).reshape(b, s, W.n_heads * W.v_dim)
     return ops.linear(o, W.o)
 

@@ -522,6 +522,44 @@ def attn_softmax_(scores: torch.Tensor, scale: float, causal: bool = True) -> to
     return scores
 
 
+def mla_attn_pack(q: torch.Tensor, kv: torch.Tensor, k_pe: torch.Tensor, cos: torch.Tensor,
+                  sin: torch.Tensor, heads: int = 16):
+    """The head-major operands of DeepSeekMLA.forward's attention (mla.py:354-366)
+    in one pass: Q = (q_nope | rope(q_pe)) [b, h, s, 192], K^T = (k_nope |
+    rope(k_pe) for every head)^T [b, h, 192, s] and V [b, h, s, 128], all
+    contiguous. q: bf16 [b, s, h*192] (q_proj output, each head nope then rope
+    part), kv: bf16 [b, s, h*256] (kv_b_proj output, each head k_nope then v),
+    k_pe: bf16 [b, s, 64] (raw shared RoPE key); each may be a view with strided
+    rows and a contiguous last dim. cos/sin: [>= s, 64] tables by position
+    (cast to bf16, as the RoPE op uses them). s must be a multiple of 8."""
+    op = "mla_attn_pack"
+    for t, nm in ((q, "q"), (kv, "kv"), (k_pe, "k_pe"), (cos, "cos"), (sin, "sin")):
+        _req(isinstance(t, torch.Tensor) and t.is_cuda, f"{op}: {nm} must be a CUDA tensor.")
+    for t, nm in ((q, "q"), (kv, "kv"), (k_pe, "k_pe")):
+        _dtype(t, torch.bfloat16, nm, op)
+        _req(t.dim() == 3 and t.stride(2) == 1, f"{op}: {nm} must be 3-D with a contiguous last dim.")
+    b, s, nq = q.shape
+    _req(nq == heads * 192 and kv.shape == (b, s, heads * 256) and k_pe.shape == (b, s, 64),
+         f"{op}: expected q [b, s, {heads}*192], kv [b, s, {heads}*256], k_pe [b, s, 64].")
+    for t, nm in ((q, "q"), (kv, "kv"), (k_pe, "k_pe")):
+        _req(b <= 1 or t.stride(0) == s * t.stride(1),
+             f"{op}: {nm} rows must be evenly spaced over batch and sequence.")
+    cb = cos.to(torch.bfloat16).contiguous()
+    sb = sin.to(torch.bfloat16).contiguous()
+    _req(cb.dim() == 2 and cb.shape[0] >= s and cb.shape[1] == 64 and sb.shape == cb.shape,
+         f"{op}: cos/sin must be [>= s, 64].")
+    dev = q.device
+    q_out = torch.empty((b, heads, s, 192), dtype=torch.bfloat16, device=dev)
+    k_t = torch.empty((b, heads, 192, s), dtype=torch.bfloat16, device=dev)
+    v = torch.empty((b, heads, s, 128), dtype=torch.bfloat16, device=dev)
+    with torch.cuda.device(dev):
+        check(lib.dsk_mla_attn_pack(q.data_ptr(), q.stride(1), kv.data_ptr(), kv.stride(1),
+                                    k_pe.data_ptr(), k_pe.stride(1), cb.data_ptr(), sb.data_ptr(),
+                                    cb.stride(0), q_out.data_ptr(), k_t.data_ptr(), v.data_ptr(),
+                                    b, s, heads, 128, 64, 128, stream_handle(dev)), op)
+    return q_out, k_t, v
+
+
 def mla_decode_attention(q_abs: torch.Tensor, q_pe: torch.Tensor, latent: torch.Tensor,
                          k_pe: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, scale: float,
                          eps: float = 1e-6, out: torch.Tensor = None,

@@ -289,6 +289,27 @@ int dsk_linear_batched(const dsk_bf16* x, int64_t ld_x, int64_t x_batch_stride,
 int dsk_attn_softmax(dsk_bf16* scores, int64_t ld, int64_t rows, int kv_len,
                      int q_len, float scale, int causal, void* stream);
 
+/* --------------------------------------------------- attention operand pack --
+ * Packs the operands of the full-sequence attention of DeepSeekMLA.forward
+ * (mla.py:354-366: query_states and key_states assembled from the nope and
+ * rotated rope parts, key_states.transpose(2, 3), value_states) in one pass:
+ *   q_out[b, h, s, 0:128]   = q[t, h*192 + 0:128]           (t = b * seq + s)
+ *   q_out[b, h, s, 128:192] = rope(q[t, h*192 + 128:192])
+ *   k_t[b, h, 0:128, s]     = kv[t, h*256 + 0:128]
+ *   k_t[b, h, 128:192, s]   = rope(k_pe[t, 0:64])          (every head)
+ *   v_out[b, h, s, :]       = kv[t, h*256 + 128:256]
+ * q, kv and k_pe are token rows (row strides ld_q, ld_kv, ld_kpe: the q_proj,
+ * kv_b_proj and kv_a_proj outputs as they leave the projections); rope is that
+ * of dsk_rope with the bf16 tables cos/sin [seq, 64] (row stride ld_cs) for
+ * positions 0..seq-1. Outputs are contiguous. Head dims nope 128, rope 64,
+ * v 128; seq % 8 == 0. The reference has no kernel for this: it replaces the
+ * reference's head-major assembly copies and the transposed read of K. */
+int dsk_mla_attn_pack(const dsk_bf16* q, int64_t ld_q, const dsk_bf16* kv,
+                      int64_t ld_kv, const dsk_bf16* k_pe, int64_t ld_kpe,
+                      const dsk_bf16* cos_t, const dsk_bf16* sin_t, int64_t ld_cs,
+                      dsk_bf16* q_out, dsk_bf16* k_t, dsk_bf16* v_out, int batch,
+                      int seq, int heads, int nope, int rope, int v_dim, void* stream);
+
 /* ----------------------------------------------- latent-cache decode attention --
  * Absorbed multi-head latent attention of new tokens over the latent KV cache
  * of LatentKVCache (src/kernels/mla_cache.py:29-219), which holds per token the

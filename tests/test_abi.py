@@ -140,6 +140,23 @@ def test_attn_softmax_validation(dsk):
     assert rc == 1 and "q_len" in _err(dsk)
 
 
+def test_attn_pack_validation(dsk):
+    lib = dsk.lib
+
+    def call(q=16, ld_q=3648, kv=16, ld_kv=4096, kpe=16, ld_kpe=3648, ld_cs=64, out=16,
+             batch=2, seq=64, heads=16, dims=(128, 64, 128)):
+        return lib.dsk_mla_attn_pack(q, ld_q, kv, ld_kv, kpe, ld_kpe, 16, 16, ld_cs, out, 16, 16,
+                                     batch, seq, heads, dims[0], dims[1], dims[2], None)
+    assert call(seq=0) == 0 and call(batch=0, q=None) == 0
+    assert call(dims=(128, 32, 128)) == 1 and "head dims" in _err(dsk)
+    assert call(seq=60) == 1 and "multiple of 8" in _err(dsk)
+    assert call(heads=70000) == 1 and "65535" in _err(dsk)
+    assert call(q=None) == 2 and "NULL" in _err(dsk)
+    assert call(out=24) == 3 and call(ld_kpe=3650) == 3
+    assert call(ld_q=3064) == 1 and "row stride" in _err(dsk)
+    assert call(ld_kv=4088) == 1 and call(ld_cs=56) == 1
+
+
 def test_mla_decode_validation(dsk):
     lib = dsk.lib
     ws = lib.dsk_mla_decode_workspace_size(1, 1, 4096)

@@ -306,6 +306,36 @@ def test_mla_projections_match_oracle(mla_setup):
         assert max_rel_err(np32(o), r) <= BF16_TOL, name
 
 
+@pytest.mark.parametrize("b,s", [(1, 8), (2, 64), (2, 72), (3, 200)])
+def test_attn_pack_is_rope_and_head_major_copies(dsk, b, s):
+    """mla_attn_pack against the composition it replaces, bitwise: Q = cat(q_nope,
+    rope(q_pe)), K^T = cat(k_nope, rope(k_pe) over heads)^T and V = v made
+    contiguous, from strided projection rows (q and k_pe slices of one
+    [b, s, 3648] buffer, kv rows padded to 4104). Lengths that are not multiples
+    of the 64-position block cover the partial last block. Q's rope part is also
+    checked against the oracle's RoPE."""
+    g = torch.Generator().manual_seed(b * 1000 + s)
+    y = torch.randn(b, s, 3648, generator=g).to(torch.bfloat16).to(DEV)
+    kvb = torch.randn(b, s, 4104, generator=g).to(torch.bfloat16).to(DEV)
+    cos = (torch.rand(s + 5, 64, generator=g) * 2 - 1)
+    sin = (torch.rand(s + 5, 64, generator=g) * 2 - 1)
+    q, kv, k_pe = y[..., :3072], kvb[..., :4096], y[..., 3584:]
+    Q, KT, V = dsk.mla_attn_pack(q, kv, k_pe, cos.to(DEV), sin.to(DEV))
+    qh = q.view(b, s, 16, 192).transpose(1, 2)
+    kvh = kv.view(b, s, 16, 256).transpose(1, 2)
+    cb = cos[:s].to(torch.bfloat16).to(DEV)[None, None].expand(b, 1, s, 64)
+    sb = sin[:s].to(torch.bfloat16).to(DEV)[None, None].expand(b, 1, s, 64)
+    q_rot, k_rot = dsk.rope(qh[..., 128:], k_pe.view(b, s, 1, 64).transpose(1, 2), cb, sb)
+    q_ref = torch.cat([qh[..., :128], q_rot], dim=-1)
+    k_ref = torch.cat([kvh[..., :128], k_rot.expand(b, 16, s, 64)], dim=-1)
+    assert Q.is_contiguous() and KT.is_contiguous() and V.is_contiguous()
+    assert torch.equal(Q, q_ref)
+    assert torch.equal(KT, k_ref.transpose(-1, -2))
+    assert torch.equal(V, kvh[..., 128:])
+    rq = ol.rope(np32(qh[..., 128:]), np32(cb), np32(sb))
+    np.testing.assert_allclose(np32(Q[..., 128:]), rq, rtol=2 ** -7, atol=2e-3)
+
+
 def test_mla_forward_matches_oracle(mla_setup):
     dm, w, W, wn = mla_setup
     b, s = 1, 128
