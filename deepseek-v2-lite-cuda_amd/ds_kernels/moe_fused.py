@@ -227,7 +227,10 @@ class FusedMoELayer(nn.Module):
         return out.view(orig)
 
 
-# id(experts) -> (packed_w1, w2), as the reference caches (moe_fused.py:224)
+# id(experts) -> (w1, w2) packed on first use, as the reference caches
+# (moe_fused.py:224); held fragment-tiled, the layout the layer kernels stream
+# fastest (the reference layout [E, 2I, H] / [E, H, I] is what prepack_experts
+# returns and what explicitly passed packed_w1 / w2 keep)
 _WEIGHT_CACHE: dict = {}
 
 
@@ -235,14 +238,19 @@ def fused_moe_forward(hidden_states: torch.Tensor, gate_weight: torch.Tensor, ex
                       top_k: int = 6, packed_w1: Optional[torch.Tensor] = None,
                       w2: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Functional form (moe_fused.py:227-272): routed experts only, like the
-    reference; weights are packed on first use and cached by id(experts)."""
+    reference; weights are packed on first use and cached by id(experts).
+    packed_w1 / w2, when given, may be in the reference layout (prepack_experts)
+    or fragment-tiled (tile_weights of it); the cached pack is tiled. Both
+    layouts give the same bits."""
     assert hidden_states.is_cuda, "hidden_states must be on CUDA."
     assert hidden_states.dim() == 2, "hidden_states must be [num_tokens, hidden_size]."
     assert hidden_states.dtype == torch.bfloat16, "hidden_states must be BF16."
     if packed_w1 is None or w2 is None:
         key = id(experts)
         if key not in _WEIGHT_CACHE:
-            _WEIGHT_CACHE[key] = prepack_experts(experts)
+            rw1, rw2 = prepack_experts(experts)
+            _WEIGHT_CACHE[key] = (tile_weights(rw1), tile_weights(rw2))
+            del rw1, rw2
         packed_w1, w2 = _WEIGHT_CACHE[key]
     logits = gate_logits(hidden_states.contiguous(), gate_weight)
     return moe_fused_forward_logits(logits, hidden_states.contiguous(), packed_w1, w2, top_k, 0,

@@ -653,8 +653,13 @@ def test_fused_moe_module_without_shared_and_functional_api(dsk, full_layer, moe
     experts = list(m.experts)
     f1 = dsk.fused_moe_forward(xd, m.gate.weight, experts, top_k=6)
     assert id(experts) in moe_fused._WEIGHT_CACHE
+    assert moe_fused._WEIGHT_CACHE[id(experts)][0].dim() == 5   # cached fragment-tiled
     f2 = dsk.fused_moe_forward(xd, m.gate.weight, experts, top_k=6)
     assert torch.equal(f1, f2)
+    # the reference layout passed explicitly: the row-major kernels, the same bits
+    rw1, rw2 = dsk.prepack_experts(experts)
+    f3 = dsk.fused_moe_forward(xd, m.gate.weight, None, 6, rw1, rw2)
+    assert torch.equal(f1, f3)
     idx_fn = om.route(dsk.moe_gate(xd, m.gate.weight).cpu().numpy(), 6)[0]
     lg32 = (x.double().numpy() @ W.wg.to(torch.bfloat16).double().numpy().T).astype(np.float32)
     ridx = om.route(lg32, 6)[0]
