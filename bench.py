@@ -232,6 +232,13 @@ def bench_mla(dsk, syn, torch, ev, reps=20, warmup=5):
     t_kvb_rs = timed(lambda: dsk.linear_rowscale(kva[..., :512], W.kvb_w, ss, 512))
     norm_bytes = 2 * rows * 512 * 2 + 512 * 4
     rope_bytes = 2 * (rows * 16 * 64 * 2) + 2 * (rows * 64 * 2) + 2 * (s * 64 * 2)
+    # the practical ceiling at these sizes: a device-to-device copy of the same
+    # number of bytes (half read, half written), by HIP-graph replay like the kernels
+    def copy_us(nbytes):
+        src = torch.empty(nbytes // 2, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        return timed(lambda: dst.copy_(src)) * 1e3
+    cp_norm, cp_rope = copy_us(norm_bytes), copy_us(rope_bytes)
     kvb_flops = 2.0 * rows * 512 * 4096
     kvb_bytes = rows * 512 * 2 + 4096 * 512 * 2 + rows * 4096 * 2
     gbs = lambda nbytes, ms: nbytes / (ms * 1e-3) / 1e9  # noqa: E731
@@ -247,10 +254,12 @@ def bench_mla(dsk, syn, torch, ev, reps=20, warmup=5):
                 "rms_norm_pass_us": t_norm * 1e3},
             "rms_norm": {"us": t_norm * 1e3, "algorithmic_bytes": norm_bytes,
                          "GB/s": gbs(norm_bytes, t_norm),
-                         "frac_of_8TB/s": gbs(norm_bytes, t_norm) / PEAK_HBM_GBS},
+                         "frac_of_8TB/s": gbs(norm_bytes, t_norm) / PEAK_HBM_GBS,
+                         "same_bytes_device_copy_us": cp_norm},
             "rope": {"us": t_rope * 1e3, "algorithmic_bytes": rope_bytes,
                      "GB/s": gbs(rope_bytes, t_rope),
-                     "frac_of_8TB/s": gbs(rope_bytes, t_rope) / PEAK_HBM_GBS},
+                     "frac_of_8TB/s": gbs(rope_bytes, t_rope) / PEAK_HBM_GBS,
+                     "same_bytes_device_copy_us": cp_rope},
             "kv_upproj": {"us": t_kvb * 1e3, "flops": kvb_flops,
                           "TFLOP/s": kvb_flops / (t_kvb * 1e-3) / 1e12,
                           "frac_of_bf16_peak": kvb_flops / (t_kvb * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
