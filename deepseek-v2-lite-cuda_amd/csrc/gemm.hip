@@ -998,11 +998,14 @@ constexpr int kSkinnyMaxRows = 64;  // largest group the small-group kernel is c
 template <int MT>
 constexpr int skinny_batch() { return MT == 1 ? 4 : 2; }
 
-template <int MT, bool SWIGLU, bool GATHER, bool TILED>
-__global__ __launch_bounds__(kSkinnyThreads) void skinny_gemm_kernel(GemmArgs p, int n_blocks) {
-  constexpr int NB = 2;  // 32-row weight blocks per workgroup
+// NB: 32-row weight blocks per workgroup (SwiGLU: the gate and the up block);
+// NW: waves per workgroup, each one slice of K.
+template <int MT, bool SWIGLU, bool GATHER, bool TILED, int NB = 2, int NW = kSkinnyWaves>
+__global__ __launch_bounds__(64 * NW) void skinny_gemm_kernel(GemmArgs p, int n_blocks) {
+  static_assert(NB == 2 || (!SWIGLU && NB == 1), "SwiGLU pairs a gate and an up block");
+  static_assert(NW == 4 || NW == 8, "reduction written for 4 or 8 waves");
   // partial sums of the upper half of the waves (8 waves), then of waves 1..3
-  __shared__ floatx4_t red[kSkinnyWaves == 8 ? 4 : 3][NB][MT][4][64];
+  __shared__ floatx4_t red[NW == 8 ? 4 : 3][NB][MT][4][64];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1053,8 +1056,8 @@ __global__ __launch_bounds__(kSkinnyThreads) void skinny_gemm_kernel(GemmArgs p,
   uint16_t* const Cg = p.C + (int64_t)g * p.c_group_stride;
   // K steps (of 16) of this wave: an even split of K/16 over the waves
   const int ksteps = p.K / 16;
-  const int s_beg = wave * ksteps / kSkinnyWaves;
-  const int nsteps = (wave + 1) * ksteps / kSkinnyWaves - s_beg;
+  const int s_beg = wave * ksteps / NW;
+  const int nsteps = (wave + 1) * ksteps / NW - s_beg;
   const int k_beg = s_beg * 16;
   // Byte offset of this lane's fragment data at k_beg in each weight block.
   // Row-major weights: row r32 of the block, 32 bytes per K step (each load
@@ -1071,7 +1074,7 @@ __global__ __launch_bounds__(kSkinnyThreads) void skinny_gemm_kernel(GemmArgs p,
         const int cb = min(nb, p.N / 32 - 1);
         rb = blk == 0 ? cb : p.up_row_offset / 32 + cb;
       } else {
-        rb = min(nb * 2 + blk, p.N / 32 - 1);
+        rb = min(nb * NB + blk, p.N / 32 - 1);
       }
       woff[blk] = (uint32_t)((((int64_t)rb * (p.K / 16) + k_beg / 16) * 512 + lane * 8) * 2);
     } else {
@@ -1080,7 +1083,7 @@ __global__ __launch_bounds__(kSkinnyThreads) void skinny_gemm_kernel(GemmArgs p,
         const int col = min(nb * 32 + r32, p.N - 1);
         row = blk == 0 ? col : p.up_row_offset + col;
       } else {
-        row = min(nb * 64 + blk * 32 + r32, p.N - 1);
+        row = min(nb * 32 * NB + blk * 32 + r32, p.N - 1);
       }
       woff[blk] = (uint32_t)(((int64_t)row * p.ldb + 8 * h + k_beg) * 2);
     }
@@ -1191,8 +1194,7 @@ __global__ __launch_bounds__(kSkinnyThreads) void skinny_gemm_kernel(GemmArgs p,
             red[slot][blk][mt][qg][lane] = v;
           }
     };
-    static_assert(kSkinnyWaves == 4 || kSkinnyWaves == 8, "reduction written for 4 or 8 waves");
-    if constexpr (kSkinnyWaves == 8) {
+    if constexpr (NW == 8) {
       if (wave >= 4) stash(wave - 4);
       __syncthreads();
       if (wave < 4) {
@@ -1219,8 +1221,8 @@ __global__ __launch_bounds__(kSkinnyThreads) void skinny_gemm_kernel(GemmArgs p,
         for (int c = 0; c < 4; ++c) v[c] += acc_read(acc[blk][mt][4 * qg + c]);
         return v;
       };
-      // a workgroup's 64 columns lie on one side of the split (n_split % 64 == 0)
-      const bool second = !SWIGLU && p.C2 != nullptr && nb * 64 >= p.n_split;
+      // a workgroup's 32 or 64 columns lie on one side of the split (n_split % 64 == 0)
+      const bool second = !SWIGLU && p.C2 != nullptr && nb * 32 * NB >= p.n_split;
       const int col0 = second ? p.n_split : 0;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
@@ -1231,7 +1233,7 @@ __global__ __launch_bounds__(kSkinnyThreads) void skinny_gemm_kernel(GemmArgs p,
         for (int j = 0; j < JN; ++j) {
 #pragma unroll
           for (int qg = 0; qg < 4; ++qg) {
-            const int nbase = SWIGLU ? nb * 32 : nb * 64 + j * 32;
+            const int nbase = SWIGLU ? nb * 32 : nb * 32 * NB + j * 32;
             const int n = nbase + 8 * qg + 4 * h;
             float v[4];
             if constexpr (SWIGLU) {
@@ -1351,6 +1353,19 @@ template <int MT, bool SWIGLU, bool GATHER, bool TILED>
 static int launch_skinny_gemm(const GemmArgs& a, hipStream_t st) {
   // groups: by offsets, or a batch of G equal groups of M rows (per-group bases)
   const int G = a.offsets != nullptr || a.a_group_stride != 0 || a.c_group_stride != 0 ? a.G : 1;
+  if constexpr (!SWIGLU) {
+    // Few groups with rows (a decode step's projections: one group, one token):
+    // 32-row blocks and 8 waves per workgroup, so the weights stream through
+    // twice the workgroups with twice the loads in flight in each.
+    const int64_t busy = a.offsets != nullptr ? std::min<int64_t>(G, std::max(a.M, 1)) : G;
+    if (busy * ((a.N + 63) / 64) < (int64_t)num_cus()) {
+      const int n_blocks = (a.N + 31) / 32;
+      hipLaunchKernelGGL((skinny_gemm_kernel<MT, SWIGLU, GATHER, TILED, 1, 8>),
+                         dim3((unsigned)((int64_t)G * n_blocks)), dim3(64 * 8), 0, st, a,
+                         n_blocks);
+      return check_launch("skinny_gemm_kernel");
+    }
+  }
   const int n_blocks = SWIGLU ? (a.N + 31) / 32 : (a.N + 63) / 64;
   const int64_t grid = (int64_t)G * n_blocks;
   hipLaunchKernelGGL((skinny_gemm_kernel<MT, SWIGLU, GATHER, TILED>), dim3((unsigned)grid),
