@@ -16,7 +16,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
 DEFAULT_OUT = os.path.join(PKG, "ds_kernels", "libdsk.so")
-SOURCES = ["dsk_errors.hip", "gate.hip", "moe_route.hip", "gemm.hip", "mla.hip", "mla_decode.hip",
+SOURCES = ["dsk_errors.hip", "gate.hip", "moe_route.hip", "gemm.hip", "gemv.hip", "mla.hip", "mla_decode.hip",
            "moe_layer.hip"]
 
 

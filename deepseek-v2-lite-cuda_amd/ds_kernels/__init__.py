@@ -10,6 +10,7 @@ from .ops import (  # noqa: F401
     linear,
     linear_batched,
     linear_rowscale,
+    linear_rows,
     linear_rowsq,
     linear_split,
     mla_attn_pack,
@@ -46,7 +47,7 @@ from .moe_fused import (  # noqa: F401
 __all__ = [
     "moe_gate", "moe_routing", "moe_scan", "moe_dispatch", "moe_combine", "swiglu", "moe_gemm1",
     "moe_gemm1_swiglu", "moe_gemm2", "rms_norm", "kv_upproj", "linear", "rope", "attn_softmax_",
-    "linear_batched", "linear_split", "linear_rowsq", "linear_rowscale", "mla_attn_pack", "mla_decode_attention", "LatentKVCache", "AbsorbedMLAWeights", "mla_decode_forward",
+    "linear_batched", "linear_rows", "linear_split", "linear_rowsq", "linear_rowscale", "mla_attn_pack", "mla_decode_attention", "LatentKVCache", "AbsorbedMLAWeights", "mla_decode_forward",
     "prepack_experts", "prepack_with_shared", "pack_tensors", "tile_weights", "untile_weights",
     "verify_prepack", "FusedMoELayer",
     "fused_moe_forward", "moe_fused_forward_logits", "moe_layer_forward",

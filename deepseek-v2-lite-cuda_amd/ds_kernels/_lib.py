@@ -46,6 +46,8 @@ SIGNATURES = {
     "dsk_mla_attn_pack": (_I, [_P, _I64, _P, _I64, _P, _I64, _P, _P, _I64, _P, _P, _P, _I, _I,
                                _I, _I, _I, _I, _P]),
     "dsk_linear_batched": (_I, [_P, _I64, _I64, _P, _P, _I64, _I64, _I, _I, _I, _I, _P]),
+    "dsk_linear_rows": (_I, [_P, _I64, _I64, _P, _I64, _P, _I64, _I64, _P, _I64, _I64, _I, _I, _I,
+                             _I, _I, _P]),
     "dsk_linear_split": (_I, [_P, _I64, _P, _P, _I64, _P, _I64, _I, _I, _I, _I, _P]),
     "dsk_mla_decode_workspace_size": (_SZ, [_I, _I, _I]),
     "dsk_mla_decode_attention": (_I, [_P, _I64, _I64, _P, _I64, _I64, _P, _P, _P, _I, _I64,

@@ -175,6 +175,11 @@ class AbsorbedMLAWeights:
 # once per new token, which a long step cannot amortise.
 UP_PROJECTED_MIN_TOKENS = 128
 
+# Decode steps of at most this many tokens run their projections on the
+# vector-ALU row kernel (dsk_linear_rows); longer ones on the small-group MFMA
+# kernel.
+ROWS_MAX_TOKENS = 4
+
 
 def _attend_up_projected(q: torch.Tensor, cache: LatentKVCache, W: MLAWeights, cos: torch.Tensor,
                          sin: torch.Tensor, eps: float) -> torch.Tensor:
@@ -252,10 +257,18 @@ def _decode_step(x: torch.Tensor, W: MLAWeights, cache: LatentKVCache, rows: tor
     T = b * n
     x2 = x.reshape(T, H)
     nq = h * (nope + r)
+    # up to 4 tokens: every projection on the vector-ALU row kernel, which
+    # spreads a one-token projection over N/8 lane groups
+    few = (T <= ROWS_MAX_TOKENS and W.q_kva is not None and W.q_kva.dim() == 4 and
+           W.o.dim() == 4 and A.uk_tiled is not None)
     if (b == 1 or n == 1) and W.q_kva is not None and W.q_kva.dim() == 4 and T <= 64:
         # q_proj and kv_a_proj in one launch, kv_a's rows straight into the slots
         q = torch.empty((T, nq), dtype=torch.bfloat16, device=x.device)
-        ops.linear_split(x2, W.q_kva, q, rows[0] if b == 1 else rows[:, 0])
+        dst = rows[0] if b == 1 else rows[:, 0]
+        if few:
+            ops.linear_rows(x2, W.q_kva, out=q, out1=dst, n_split=nq)
+        else:
+            ops.linear_split(x2, W.q_kva, q, dst)
         q = q.view(T, h, nope + r)                         # [T, h, 192]
     else:
         q = ops.linear(x, W.q).view(T, h, nope + r)
@@ -269,7 +282,9 @@ def _decode_step(x: torch.Tensor, W: MLAWeights, cache: LatentKVCache, rows: tor
         return ops.linear(o, W.o)
     latent, k_pe = cache.get(L)
     small = T <= 64 and A.uk_tiled is not None
-    if small:   # per-head products on strided views, one launch each
+    if few:
+        q_abs = ops.linear_rows(q[..., :nope].transpose(0, 1), A.uk_tiled)     # [h, T, lora]
+    elif small:   # per-head products on strided views, one launch each
         q_abs = ops.linear_batched(q[..., :nope].transpose(0, 1), A.uk_tiled)  # [h, T, lora]
     else:
         q_abs = torch.bmm(q[..., :nope].transpose(0, 1).contiguous(), A.w_uk)
@@ -280,7 +295,10 @@ def _decode_step(x: torch.Tensor, W: MLAWeights, cache: LatentKVCache, rows: tor
     cache._rope_len = L          # the kernel rotated and stored the new keys
     if small:   # o[t, h*v:(h+1)*v] = o_lat[h, t] @ (W_UV[h] * w)^T, written token-major
         o = torch.empty((T, h * vd), dtype=torch.bfloat16, device=x.device)
-        ops.linear_batched(o_lat, A.uv_tiled, out=o.view(T, h, vd).transpose(0, 1))
+        (ops.linear_rows if few else ops.linear_batched)(o_lat, A.uv_tiled,
+                                                         out=o.view(T, h, vd).transpose(0, 1))
     else:
         o = torch.bmm(o_lat, A.w_uv_t).transpose(0, 1).reshape(T, h * vd)
+    if few:
+        return ops.linear_rows(o, W.o).view(b, n, -1)
     return ops.linear(o, W.o).view(b, n, -1)

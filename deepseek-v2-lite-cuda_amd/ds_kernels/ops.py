@@ -421,6 +421,47 @@ def linear_batched(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor = No
     return out
 
 
+def linear_rows(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor = None,
+                out1: torch.Tensor = None, n_split: int = None) -> torch.Tensor:
+    """x @ weight^T for at most 4 token rows on the vector ALU (dsk_linear_rows),
+    spread over N/8 lane groups: the projections of a one-token decode step.
+    x: bf16 [M, K] or [batch, M, K] (contiguous last dim); weight: fragment-tiled
+    [N/32, K/16, 64, 8] or [batch, N/32, K/16, 64, 8]; out: optional destination
+    view ([.., M, n_split] when out1 is given); out1 with n_split: columns
+    n_split.. go to out1 ([.., M, N - n_split]). Returns out."""
+    op = "linear_rows"
+    batched = x.dim() == 3
+    _req(x.is_cuda and x.dtype == torch.bfloat16 and x.dim() in (2, 3) and x.stride(-1) == 1,
+         f"{op}: x must be a bf16 CUDA tensor [M, K] or [batch, M, K] with a contiguous last dim.")
+    xb = x if batched else x[None]
+    nb, M, K = xb.shape
+    wb = weight if weight.dim() == 5 else weight[None]
+    _req(weight.is_cuda and weight.is_contiguous() and weight.dtype == torch.bfloat16 and
+         wb.dim() == 5 and wb.shape[0] == nb and tuple(wb.shape[3:]) == (64, 8) and
+         wb.shape[2] * 16 == K, f"{op}: weight must be tiled [N/32, {K // 16}, 64, 8] per entry.")
+    N = wb.shape[1] * 32
+    ns = N if out1 is None else n_split
+    _req(ns is not None and 0 <= ns <= N, f"{op}: n_split must be in [0, N] with out1.")
+    shape0 = (nb, M, ns) if batched else (M, ns)
+    if out is None:
+        out = torch.empty(shape0, dtype=torch.bfloat16, device=x.device)
+    for t, shp, nm in ((out, shape0, "out"),) + (((out1, (nb, M, N - ns) if batched else
+                                                  (M, N - ns), "out1"),) if out1 is not None else ()):
+        _req(t.is_cuda and t.dtype == torch.bfloat16 and tuple(t.shape) == shp and t.stride(-1) == 1,
+             f"{op}: {nm} must be bf16 {list(shp)} with a contiguous last dim.")
+    o0 = out if batched else out[None]
+    o1 = (out1 if batched else out1[None]) if out1 is not None else None
+    if nb and M:
+        with torch.cuda.device(x.device):
+            check(lib.dsk_linear_rows(xb.data_ptr(), xb.stride(1), xb.stride(0), wb.data_ptr(),
+                                      wb[0].numel() if nb > 1 else 0, o0.data_ptr(), o0.stride(1),
+                                      o0.stride(0), o1.data_ptr() if o1 is not None else None,
+                                      o1.stride(1) if o1 is not None else 0,
+                                      o1.stride(0) if o1 is not None else 0, ns, nb, M, K, N,
+                                      stream_handle(x.device)), op)
+    return out
+
+
 def kv_upproj(normed_kv: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """kv_b_proj up-projection (kv_upproj.cu:133-178): [..., 512] -> [..., out_dim].
     weight is [out_dim, kv_lora_rank] as in the reference, or its fragment-tiled

@@ -263,6 +263,23 @@ int dsk_linear_split(const dsk_bf16* x, int64_t ld_x, const dsk_bf16* w_tiled,
                      dsk_bf16* out0, int64_t ld_out0, dsk_bf16* out1, int64_t ld_out1,
                      int M, int K, int N, int n_split, void* stream);
 
+/* ------------------------------------------------------- few-row linear --
+ * out[b][m][n] = sum_k x[b][m][k] * w[b][n][k] for M <= 4 token rows, with w
+ * fragment-tiled [batch, N/32, K/16, 64, 8] (K % 128 == 0, N % 32 == 0), fp32
+ * sums rounded once to bf16. Entry b of x starts x_batch_stride elements
+ * after entry b-1, rows ld_x apart; outputs n < n_split go to out0 (row pitch
+ * ld_out0, entry stride out0_batch_stride), the others to out1 at column
+ * n - n_split (n_split = N: out1 unused). Vector-ALU dot products over 8 weight
+ * rows per lane group, so a one-token projection of N rows runs as N/8 lane
+ * groups instead of N/32 workgroups: the q/kv_a, per-head and o projections of
+ * a one-token absorbed-MLA decode step. The reference has no counterpart (it
+ * runs its projections as torch GEMMs and has no decode step). */
+int dsk_linear_rows(const dsk_bf16* x, int64_t ld_x, int64_t x_batch_stride,
+                    const dsk_bf16* w_tiled, int64_t w_batch_stride, dsk_bf16* out0,
+                    int64_t ld_out0, int64_t out0_batch_stride, dsk_bf16* out1,
+                    int64_t ld_out1, int64_t out1_batch_stride, int n_split, int batch,
+                    int M, int K, int N, void* stream);
+
 /* --------------------------------------------------------- batched linear --
  * out[b] = x[b] @ w[b]^T for b < batch, with M <= 64 rows per entry (the
  * weight-streaming small-group kernel; one launch for all entries). Entry b of

@@ -140,6 +140,23 @@ def test_attn_softmax_validation(dsk):
     assert rc == 1 and "q_len" in _err(dsk)
 
 
+def test_linear_rows_validation(dsk):
+    lib = dsk.lib
+
+    def call(M=1, K=2048, N=2048, n_split=2048, x=16, ld_x=2048, out0=16, out1=None, batch=1):
+        return lib.dsk_linear_rows(x, ld_x, 0, 16, 0, out0, 2048, 0, out1, 0, 0, n_split, batch,
+                                   M, K, N, None)
+    assert call(M=0) == 0 and call(batch=0, x=None) == 0
+    assert call(M=5) == 1 and "4 token rows" in _err(dsk)
+    assert call(K=2000) == 1 and "multiple of 128" in _err(dsk)
+    assert call(N=2040, n_split=2040) == 1 and "multiple of 128" in _err(dsk)
+    assert call(n_split=2049) == 1 and "n_split" in _err(dsk)
+    assert call(n_split=1024) == 2 and "NULL" in _err(dsk)
+    assert call(x=None) == 2
+    assert call(x=24) == 3 and call(ld_x=2052) == 3
+    assert call(ld_x=1024, K=2048) == 1 and "row stride" in _err(dsk)
+
+
 def test_attn_pack_validation(dsk):
     lib = dsk.lib
 

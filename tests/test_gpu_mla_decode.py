@@ -197,6 +197,55 @@ def test_linear_batched_strided_views(setup, M, K, N):
     assert torch.count_nonzero(out_full[..., N:]) == 0   # nothing written past the slice
 
 
+@pytest.mark.parametrize("M,K,N", [(1, 2048, 3648), (2, 2048, 2048), (4, 2048, 64), (3, 512, 128),
+                                   (1, 128, 512), (4, 128, 96), (1, 640, 32)])
+def test_linear_rows_matches_fp32(setup, M, K, N):
+    """dsk_linear_rows (vector ALU, 8 weight rows per lane group) against an fp32
+    reference of the same bf16 operands: one entry with x rows strided inside a
+    wider buffer, and 3 batched entries on strided views; the same bits on a
+    second call; K = 128 and 640 take the 16-lane path (four row groups per wave;
+    K = 640 with five K chunks per lane)."""
+    dsk = setup[0]
+    g = torch.Generator().manual_seed(M * 31 + K + N)
+    xb = torch.randn(M, K + 32, generator=g).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16)
+    x = xb.to(DEV)[:, :K]
+    out = dsk.linear_rows(x, dsk.tile_weights(w[None].to(DEV))[0])
+    ref = xb[:, :K].float() @ w.float().T
+    assert out.shape == (M, N)
+    assert max_rel_err(np32(out), ref.numpy()) <= BF16_TOL
+    again = dsk.linear_rows(x, dsk.tile_weights(w[None].to(DEV))[0])
+    assert torch.equal(out, again)
+    # batched, strided in and out
+    big = torch.randn(M, 3, K + 64, generator=g).to(torch.bfloat16)
+    wb = (torch.randn(3, N, K, generator=g) * 0.05).to(torch.bfloat16)
+    xs = big.to(DEV)[..., :K].transpose(0, 1)                       # [3, M, K] strided
+    out_full = torch.zeros(M, 3, N + 8, dtype=torch.bfloat16, device=DEV)
+    o = out_full[..., :N].transpose(0, 1)                            # [3, M, N] strided
+    dsk.linear_rows(xs, dsk.tile_weights(wb.to(DEV)), out=o)
+    refb = torch.einsum("hmk,hnk->hmn", big[..., :K].transpose(0, 1).float(), wb.float())
+    assert max_rel_err(np32(o), refb.numpy()) <= BF16_TOL
+    assert torch.count_nonzero(out_full[..., N:]) == 0
+
+
+@pytest.mark.parametrize("M,n0", [(1, 3072), (4, 64), (2, 0)])
+def test_linear_rows_split_output(setup, M, n0):
+    """The two-destination form used for q_proj + kv_a_proj: columns from n0 go to
+    a strided second buffer; equal to the one-output call bit for bit."""
+    dsk = setup[0]
+    g = torch.Generator().manual_seed(M + n0)
+    x = torch.randn(M, 2048, generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(3648, 2048, generator=g) * 0.02).to(torch.bfloat16)
+    wt = dsk.tile_weights(w[None])[0].to(DEV)
+    full = dsk.linear_rows(x, wt)
+    out0 = torch.empty(M, n0, dtype=torch.bfloat16, device=DEV)
+    pad = torch.zeros(M, 3648 - n0 + 64, dtype=torch.bfloat16, device=DEV)
+    dsk.linear_rows(x, wt, out=out0, out1=pad[:, :3648 - n0], n_split=n0)
+    assert torch.equal(out0, full[:, :n0])
+    assert torch.equal(pad[:, :3648 - n0], full[:, n0:])
+    assert torch.count_nonzero(pad[:, 3648 - n0:]) == 0
+
+
 @pytest.mark.parametrize("M,n0", [(1, 3072), (16, 3072), (64, 64), (100, 3072)])
 def test_linear_split_matches_linear(setup, M, n0):
     """dsk_linear_split (one small-group launch for M <= 64, two launches over the
