@@ -986,7 +986,11 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void wide_gemm_kernel(GemmArgs 
 //     latency; with fragment-tiled weights every load is 1 KB contiguous;
 //   * the partial sums meet in LDS once at the end, in a fixed order (waves
 //     1-3 into wave 0), and wave 0 applies the epilogue (SwiGLU from fp32
-//     accumulators).
+//     accumulators);
+//   * when so few (group, 64-row) units exist that they do not cover the CUs
+//     (a projection of one or a few tokens), plain products switch to 32
+//     weight rows and 8 waves per workgroup (NB = 1, NW = 8): twice the
+//     workgroups, each splitting K eight ways.
 // The weights are MFMA operand A and the tokens operand B, as in the large
 // kernel, so the output layout per lane is the same (4 consecutive columns).
 constexpr int kSkinnyWaves = 4;  // waves per workgroup, each one slice of K
