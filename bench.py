@@ -98,8 +98,11 @@ def bench_prefill(dsk, syn, torch, F, W, packed, T, steps, warmup, ev):
     for e in events:
         ev.destroy(e)
     mean = lambda v: sum(v) / len(v)  # noqa: E731
+    per_step = sorted(sum(s) for s in stage)  # first to last stage event of each step
     return {
         "ms_per_step": elapsed * 1e3 / steps,
+        "step_ms_median": per_step[len(per_step) // 2],
+        "step_ms_p95": per_step[min(len(per_step) - 1, int(0.95 * len(per_step)))],
         "gate_route_ms": mean([s[0] for s in stage]),
         "gemm1_ms": mean([s[1] for s in stage]),
         "gemm2_ms": mean([s[2] for s in stage]),
@@ -546,7 +549,8 @@ def main():
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": ach_g1 / PEAK_BF16_TFLOPS, "traffic": traffic,
                      "flops_per_launch": flops_g1, "mean_launch_ms": pre["gemm1_ms"]},
-        "stages_ms": {k: pre[k] for k in ("gate_route_ms", "gemm1_ms", "gemm2_ms", "combine_ms")},
+        "stages_ms": {k: pre[k] for k in ("gate_route_ms", "gemm1_ms", "gemm2_ms", "combine_ms",
+                                          "step_ms_median", "step_ms_p95")},
         "gemm2": {"achieved_tflops": ach_g2, "frac": ach_g2 / PEAK_BF16_TFLOPS},
         "gemms_combined": {"achieved_tflops": ach_both, "frac": ach_both / PEAK_BF16_TFLOPS},
     }
