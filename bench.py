@@ -337,6 +337,18 @@ def bench_latent_decode(dsk, torch, dm, W, timed, dev, g):
         dsk.mla_decode_forward(x1, W, cache, cos, sin, A)
 
     t_step = timed(step)
+    # four sequences at once: one new token each (the few-row projections at 4 rows)
+    x4 = torch.randn(4, L, 2048, generator=g).to(torch.bfloat16).to(dev)
+    cache4 = dsk.LatentKVCache.for_inference(4, max_seq=L, device=dev)
+    dsk.mla_decode_forward(x4[:, :L - 1], W, cache4, cos, sin, A)
+    x41 = x4[:, L - 1:].contiguous()
+
+    def step4():
+        cache4._len = L - 1
+        dsk.mla_decode_forward(x41, W, cache4, cos, sin, A)
+
+    t_step4 = timed(step4)
+    del x4, cache4, x41
     cf, sf = dm.yarn_cos_sin(L, device=dev)
     t_full = timed(lambda: dm.mla_forward(x, W, cf, sf), per_graph=1)
     res["decode_step"] = {"batch": 1, "cache_len": L, "us": t_step * 1e3,
@@ -344,6 +356,8 @@ def bench_latent_decode(dsk, torch, dm, W, timed, dev, g):
                           "note": "one new token: q / kv_a projections, cache append, absorbed "
                                   "attention, W_UV, o_proj; versus mla_forward over all 4096 "
                                   "positions (what a forward without a cache recomputes)"}
+    res["decode_step_b4"] = {"batch": 4, "cache_len": L, "us": t_step4 * 1e3,
+                             "note": "one new token in each of 4 sequences, same step"}
     return res
 
 
