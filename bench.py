@@ -22,7 +22,7 @@ Also reported on the same line:
                 on this host's cores: the same T=4096 workload (2 calls, fp32; the
                 reported value) and config 0 (T=64) beside it.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+Usage: python bench.py [--gpus 1] [--steps K (200)] [--warmup W (20)]
                        [--profile | --decode-only T | --mla-only | --mla-decode-only]
 """
 from __future__ import annotations
@@ -470,8 +470,11 @@ def main():
         return
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # 20 warm-up + 200 timed steps, as the reference's benchmark
+    # (tests/benchmark_moe_performance.py:50-51); after a cold start the layer
+    # step takes ~15 steps to settle (clocks and caches)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--tokens", type=int, default=4096)
     ap.add_argument("--decode-steps", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
