@@ -56,6 +56,9 @@ def _run_steps(setup, x, steps):
     (1, [700, 1, 5]),                  # many blocks (700 is not a multiple of 8: absorbed kernel)
     (2, [256, 1, 130]),                # prompt through up-projected K/V, then the kernel (merge)
     (1, [1, 255, 8]),                  # up-projected step over a one-token prefix
+    (3, [40, 1, 1]),                   # 3 sequences: the few-row projections at 3 rows
+    (4, [100, 1, 1]),                  # 4 sequences: the few-row projections at 4 rows
+    (1, [30, 3, 4, 5]),                # 3 and 4 new tokens of one sequence, then 5 (MFMA path)
 ])
 def test_decode_matches_full_sequence_oracle(setup, b, steps):
     S = sum(steps)
