@@ -426,7 +426,8 @@ def linear_rows(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor = None,
     """x @ weight^T for at most 4 token rows on the vector ALU (dsk_linear_rows),
     spread over N/8 lane groups: the projections of a one-token decode step.
     x: bf16 [M, K] or [batch, M, K] (contiguous last dim); weight: fragment-tiled
-    [N/32, K/16, 64, 8] or [batch, N/32, K/16, 64, 8]; out: optional destination
+    [N/32, K/16, 64, 8] (shared by every batch entry) or [batch, N/32, K/16, 64,
+    8]; out: optional destination
     view ([.., M, n_split] when out1 is given); out1 with n_split: columns
     n_split.. go to out1 ([.., M, N - n_split]). Returns out."""
     op = "linear_rows"
@@ -437,7 +438,7 @@ def linear_rows(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor = None,
     nb, M, K = xb.shape
     wb = weight if weight.dim() == 5 else weight[None]
     _req(weight.is_cuda and weight.is_contiguous() and weight.dtype == torch.bfloat16 and
-         wb.dim() == 5 and wb.shape[0] == nb and tuple(wb.shape[3:]) == (64, 8) and
+         wb.dim() == 5 and wb.shape[0] in (1, nb) and tuple(wb.shape[3:]) == (64, 8) and
          wb.shape[2] * 16 == K, f"{op}: weight must be tiled [N/32, {K // 16}, 64, 8] per entry.")
     N = wb.shape[1] * 32
     ns = N if out1 is None else n_split
@@ -454,7 +455,8 @@ def linear_rows(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor = None,
     if nb and M:
         with torch.cuda.device(x.device):
             check(lib.dsk_linear_rows(xb.data_ptr(), xb.stride(1), xb.stride(0), wb.data_ptr(),
-                                      wb[0].numel() if nb > 1 else 0, o0.data_ptr(), o0.stride(1),
+                                      wb[0].numel() if wb.shape[0] > 1 else 0, o0.data_ptr(),
+                                      o0.stride(1),
                                       o0.stride(0), o1.data_ptr() if o1 is not None else None,
                                       o1.stride(1) if o1 is not None else 0,
                                       o1.stride(0) if o1 is not None else 0, ns, nb, M, K, N,

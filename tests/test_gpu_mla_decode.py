@@ -206,8 +206,8 @@ def test_linear_rows_matches_fp32(setup, M, K, N):
     """dsk_linear_rows (vector ALU, 8 weight rows per lane group) against an fp32
     reference of the same bf16 operands: one entry with x rows strided inside a
     wider buffer, and 3 batched entries on strided views; the same bits on a
-    second call; K = 128 and 640 take the 16-lane path (four row groups per wave;
-    K = 640 with five K chunks per lane)."""
+    second call; one weight shared by 3 batched entries; K = 128 and 640 take the
+    16-lane path (four row groups per wave; K = 640 with five K chunks per lane)."""
     dsk = setup[0]
     g = torch.Generator().manual_seed(M * 31 + K + N)
     xb = torch.randn(M, K + 32, generator=g).to(torch.bfloat16)
@@ -229,6 +229,12 @@ def test_linear_rows_matches_fp32(setup, M, K, N):
     refb = torch.einsum("hmk,hnk->hmn", big[..., :K].transpose(0, 1).float(), wb.float())
     assert max_rel_err(np32(o), refb.numpy()) <= BF16_TOL
     assert torch.count_nonzero(out_full[..., N:]) == 0
+    # batched x with one weight shared by every entry (weight batch stride 0)
+    shared = dsk.linear_rows(xs, dsk.tile_weights(w[None].to(DEV))[0])
+    refs = big[..., :K].transpose(0, 1).float() @ w.float().T
+    assert shared.shape == (3, M, N)
+    assert max_rel_err(np32(shared), refs.numpy()) <= BF16_TOL
+    assert torch.equal(shared[0], dsk.linear_rows(xs[0], dsk.tile_weights(w[None].to(DEV))[0]))
 
 
 @pytest.mark.parametrize("M,n0", [(1, 3072), (4, 64), (2, 0)])
