@@ -43,7 +43,30 @@ struct GemmArgs {
   int64_t ld_rowscale;
   int rowscale_parts, rowscale_cols;
   float rowscale_eps;
+  // Small-group SwiGLU kernel with gathered rows, optional (decode steps of at
+  // most kRouteInGemmTokens tokens): every workgroup routes the step itself in
+  // its prologue from the gate's partial planes (route_token), and uses its own
+  // expert offsets and row map instead of offsets / a_rows; workgroup 0 also
+  // writes the routing outputs (topk idx / weights, counts, offsets with the
+  // always-on groups, token_map, slot_of) for the kernels after it.
+  const float* rt_parts;
+  int rt_n_parts;
+  int64_t rt_part_stride;
+  const float* rt_bias;
+  int rt_T, rt_E, rt_K, rt_nsh;
+  int32_t* rt_idx;
+  float* rt_w;
+  int32_t* rt_counts;
+  int32_t* rt_offsets;
+  int32_t* rt_token_map;
+  int32_t* rt_slot_of;
 };
+
+// Tokens up to which a decode step is routed in GEMM1's prologue: every launched
+// workgroup routes before it knows whether its group is busy, and at T = 1 the
+// grid holds only busy groups (at most T*K + always-on groups of rows).
+constexpr int kRouteInGemmTokens = 1;
+constexpr int kRouteInGemmSlots = 256;  // routed + always-on rows the prologue maps
 
 int run_gemm(const GemmArgs& a, bool swiglu, hipStream_t st);
 

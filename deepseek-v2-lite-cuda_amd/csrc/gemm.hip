@@ -47,6 +47,7 @@
 // silu(gate) * up is computed from fp32 accumulators held by the same lane.
 #include "dsk_internal.hpp"
 #include "gemm_sched.hpp"
+#include "route_token.hpp"
 
 #include <algorithm>
 #include <atomic>
@@ -1002,6 +1003,72 @@ constexpr int kSkinnyMaxRows = 64;  // largest group the small-group kernel is c
 template <int MT>
 constexpr int skinny_batch() { return MT == 1 ? 4 : 2; }
 
+// Routing of a decode step (at most kRouteInGemmTokens tokens) in the prologue
+// of the small-group SwiGLU kernel, as route_kernel does it for one chunk: the
+// 16-lane row g of wave w picks the experts of token 4 w + g (route_token);
+// 64-bit expert masks in the LDS give each (token, k) its stable slot (expert-
+// major, ascending token) and the offsets of the routed groups, followed by
+// the always-on groups of T rows each. Every workgroup computes the same
+// integers from the same planes; workgroup 0 also stores them for the kernels
+// after this one.
+__device__ __forceinline__ void skinny_route_prologue(const GemmArgs& p,
+                                                      unsigned long long* rt_mask, int* rt_off,
+                                                      int* rt_tok, int lane, int wave) {
+  const int T = p.rt_T, E = p.rt_E, K = p.rt_K, nsh = p.rt_nsh;
+  const bool store = blockIdx.x == 0;
+  if (threadIdx.x < 64) rt_mask[threadIdx.x] = 0ull;
+  __syncthreads();
+  const int j = lane & 15;
+  const int tl = 4 * wave + (lane >> 4);
+  int my_e;
+  float my_w;
+  route_token(p.rt_parts, E, p.rt_n_parts, p.rt_part_stride, p.rt_bias, tl, tl < T,
+              4 * wave < T, E, K, lane, my_e, my_w);
+  if (tl < T && j < K) {
+    atomicOr(&rt_mask[my_e], 1ull << tl);
+    if (store) {
+      p.rt_idx[tl * K + j] = my_e;
+      p.rt_w[tl * K + j] = my_w;
+    }
+  } else {
+    my_e = -1;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const int c = lane < E ? __popcll(rt_mask[lane]) : 0;
+    const int inc = wave_inclusive_scan(c);
+    if (lane < E) {
+      rt_off[lane] = inc - c;
+      if (store) {
+        p.rt_offsets[lane] = inc - c;
+        p.rt_counts[lane] = c;
+      }
+    }
+    if (lane == 63) {
+      for (int x = 0; x <= nsh; ++x) {
+        rt_off[E + x] = inc + x * T;
+        if (store) p.rt_offsets[E + x] = inc + x * T;
+      }
+    }
+  }
+  __syncthreads();
+  if (my_e >= 0) {
+    const int slot = rt_off[my_e] + __popcll(rt_mask[my_e] & ((1ull << tl) - 1ull));
+    rt_tok[slot] = tl;
+    if (store) {
+      p.rt_token_map[slot] = tl;
+      p.rt_slot_of[tl * K + j] = slot;
+    }
+  }
+  // rows of the always-on groups: group E+x row t is token t
+  const int S = T * K;
+  for (int r = threadIdx.x; r < nsh * T; r += blockDim.x) {
+    rt_tok[S + r] = r % T;
+    if (store) p.rt_token_map[S + r] = r % T;
+  }
+  __syncthreads();
+}
+
 // NB: 32-row weight blocks per workgroup (SwiGLU: the gate and the up block);
 // NW: waves per workgroup, each one slice of K.
 template <int MT, bool SWIGLU, bool GATHER, bool TILED, int NB = 2, int NW = kSkinnyWaves>
@@ -1010,26 +1077,41 @@ __global__ __launch_bounds__(64 * NW) void skinny_gemm_kernel(GemmArgs p, int n_
   static_assert(NW == 4 || NW == 8, "reduction written for 4 or 8 waves");
   // partial sums of the upper half of the waves (8 waves), then of waves 1..3
   __shared__ floatx4_t red[NW == 8 ? 4 : 3][NB][MT][4][64];
+  // routing in the prologue (SwiGLU with gathered rows only): expert masks of
+  // the step's tokens, group offsets and the slot -> token map
+  constexpr bool kCanRoute = SWIGLU && GATHER && NW == 4;
+  __shared__ unsigned long long rt_mask[kCanRoute ? 64 : 1];
+  __shared__ int rt_off[kCanRoute ? kMaxGroups + 1 : 1];
+  __shared__ int rt_tok[kCanRoute ? kRouteInGemmSlots : 1];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  bool routed = false;
+  if constexpr (kCanRoute) {
+    if (p.rt_parts != nullptr) {
+      routed = true;
+      skinny_route_prologue(p, rt_mask, rt_off, rt_tok, lane, wave);
+    }
+  }
+  auto group_offset = [&](int i) { return routed ? rt_off[i] : p.offsets[i]; };
   int g = blockIdx.x / n_blocks;
   const int nb = blockIdx.x - g * n_blocks;
   int mb = 0, me = p.M;
   if (p.offsets != nullptr) {
-    // The grid holds n_blocks workgroups per group, but only non-empty groups
-    // have work: workgroup ordinal g takes the g-th non-empty group. The busy
+    // The grid holds n_blocks workgroups for each of min(G, M) group ordinals
+    // (no more groups than rows can be busy), but only non-empty groups have
+    // work: workgroup ordinal g takes the g-th non-empty group. The busy
     // workgroups thus come first in dispatch order, and the idle ones, all at
     // the end of the grid, do not hold workgroup slots between them.
-    const int G = gridDim.x / n_blocks;
+    const int G = p.G;
     int ord = g;
     g = -1;
     for (int base = 0; base < G; base += 64) {
       const int gi = base + lane;
       int lo = 0, hi = 0;
       if (gi < G) {
-        lo = min(max(p.offsets[gi], 0), p.M);
-        hi = min(max(p.offsets[gi + 1], lo), p.M);
+        lo = min(max(group_offset(gi), 0), p.M);
+        hi = min(max(group_offset(gi + 1), lo), p.M);
       }
       const bool busy = hi > lo;
       const uint64_t mask = __ballot(busy);
@@ -1100,7 +1182,7 @@ __global__ __launch_bounds__(64 * NW) void skinny_gemm_kernel(GemmArgs p, int n_
     for (int mt = 0; mt < MT; ++mt) {
       const int m = m0 + mt * 32 + r32;
       const int mm = m < me ? m : m0;
-      int row = GATHER ? p.a_rows[mm] : mm;
+      int row = GATHER ? (routed ? rt_tok[mm] : p.a_rows[mm]) : mm;
       row = (row >= 0 && row < row_limit) ? row : 0;
       toff[mt] = (uint32_t)(((int64_t)row * p.lda + 8 * h + k_beg) * 2);
     }
@@ -1357,6 +1439,8 @@ template <int MT, bool SWIGLU, bool GATHER, bool TILED>
 static int launch_skinny_gemm(const GemmArgs& a, hipStream_t st) {
   // groups: by offsets, or a batch of G equal groups of M rows (per-group bases)
   const int G = a.offsets != nullptr || a.a_group_stride != 0 || a.c_group_stride != 0 ? a.G : 1;
+  // group ordinals launched: with offsets, at most one busy group per row
+  const int64_t GL = a.offsets != nullptr ? std::min<int64_t>(G, std::max(a.M, 1)) : G;
   if constexpr (!SWIGLU) {
     // Few groups with rows (a decode step's projections: one group, one token):
     // 32-row blocks and 8 waves per workgroup, so the weights stream through
@@ -1365,13 +1449,12 @@ static int launch_skinny_gemm(const GemmArgs& a, hipStream_t st) {
     if (busy * ((a.N + 63) / 64) < (int64_t)num_cus()) {
       const int n_blocks = (a.N + 31) / 32;
       hipLaunchKernelGGL((skinny_gemm_kernel<MT, SWIGLU, GATHER, TILED, 1, 8>),
-                         dim3((unsigned)((int64_t)G * n_blocks)), dim3(64 * 8), 0, st, a,
-                         n_blocks);
+                         dim3((unsigned)(GL * n_blocks)), dim3(64 * 8), 0, st, a, n_blocks);
       return check_launch("skinny_gemm_kernel");
     }
   }
   const int n_blocks = SWIGLU ? (a.N + 31) / 32 : (a.N + 63) / 64;
-  const int64_t grid = (int64_t)G * n_blocks;
+  const int64_t grid = GL * n_blocks;
   hipLaunchKernelGGL((skinny_gemm_kernel<MT, SWIGLU, GATHER, TILED>), dim3((unsigned)grid),
                      dim3(kSkinnyThreads), 0, st, a, n_blocks);
   return check_launch("skinny_gemm_kernel");

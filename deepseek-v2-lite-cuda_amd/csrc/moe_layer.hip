@@ -15,6 +15,7 @@
 // Slot layout: [0, T*K) routed (expert-major, ascending token), then group E+j
 // rows [T*K + j*T, T*K + (j+1)*T) in token order.
 #include "dsk_internal.hpp"
+#include "route_token.hpp"
 
 #include <atomic>
 #include <mutex>
@@ -82,7 +83,18 @@ static int layer_after_gate(const float* logits, int n_parts, int64_t part_strid
     return DSK_OK;
   };
   int rc;
-  if (nblk == 1) {
+  // Decode steps of at most kRouteInGemmTokens tokens: GEMM1's prologue does the
+  // routing (every workgroup for itself, workgroup 0 storing the results), so
+  // no route launch runs before it.
+#ifndef DSK_ROUTE_IN_GEMM
+#define DSK_ROUTE_IN_GEMM 1
+#endif
+  const bool route_in_gemm = DSK_ROUTE_IN_GEMM && nblk == 1 && T <= kRouteInGemmTokens &&
+                             Stot <= kRouteInGemmSlots &&
+                             n_parts >= 1 && n_parts <= kMaxGateParts;
+  if (route_in_gemm) {
+    // nothing to launch here
+  } else if (nblk == 1) {
     rc = launch_route(logits, E, n_parts, part_stride, bias, T, E, K, idx, w, hist, rank,
                       counts, offsets, token_map, slot_of, nsh, st);
     if (rc) return rc;
@@ -107,6 +119,22 @@ static int layer_after_gate(const float* logits, int n_parts, int64_t part_strid
   g1.up_row_offset = I;
   g1.max_group_rows = T;  // a token routes to an expert at most once; shared groups hold T
   g1.b_tiled = weight_layout == DSK_LAYOUT_TILED;
+  if (route_in_gemm) {
+    g1.rt_parts = logits;
+    g1.rt_n_parts = n_parts;
+    g1.rt_part_stride = part_stride;
+    g1.rt_bias = bias;
+    g1.rt_T = T;
+    g1.rt_E = E;
+    g1.rt_K = K;
+    g1.rt_nsh = nsh;
+    g1.rt_idx = idx;
+    g1.rt_w = w;
+    g1.rt_counts = counts;
+    g1.rt_offsets = offsets;
+    g1.rt_token_map = token_map;
+    g1.rt_slot_of = slot_of;
+  }
   if ((rc = run_gemm(g1, true, st))) return rc;
   if ((rc = mark(2))) return rc;
 

@@ -14,6 +14,7 @@
 //   slot = offsets[e] + chunk_base[chunk][e] + rank,
 // which is deterministic and needs no atomics beyond LDS bit-ors.
 #include "dsk_internal.hpp"
+#include "route_token.hpp"
 
 #include <algorithm>
 #include <climits>
@@ -25,7 +26,6 @@ constexpr int kRouteThreads = 1024;   // 16 waves, 4 tokens each
 constexpr int kRouteWaves = kRouteThreads / kWave;
 constexpr int kTokPerWave = kChunk / kRouteWaves;  // one per 16-lane row
 constexpr int kRankThreads = 256;
-constexpr int kMaxGateParts = 16;  // partial gate-sum planes the route kernel adds
 
 // ------------------------------------------------------------------ route --
 // Four tokens per wave (one per 16-lane row). Writes topk idx / weights,
@@ -51,72 +51,17 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(
 
   const int t0 = blockIdx.x * kChunk;
   // Four tokens per wave at once: the 16 lanes of row g hold token
-  // tl = 4 * wave + g, lane j the logits of experts j, j+16, j+32, j+48, so
-  // every reduction is a 4-value local step plus a 16-lane DPP step.
+  // tl = 4 * wave + g (route_token).
   const int g = lane >> 4, j = lane & 15;
   const int tl = kTokPerWave * wave + g;
   const int t = t0 + tl;
   const bool active = t < T;  // uniform over the 16-lane row
-  float xv[4];
-  bool taken[4];
-  // logits = sum of n_parts partial sums (K slices of the gate GEMM) in a
-  // fixed order, plus the optional per-expert bias
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int e = j + 16 * q;
-    taken[q] = e >= E;  // padding experts are never chosen
-    float v = -INFINITY;
-    if (active && e < E) {
-      // all plane loads issued first, then summed in plane order
-      const float* src = logits + (int64_t)t * ld + e;
-      float pv[kMaxGateParts];
-#pragma unroll
-      for (int s = 0; s < kMaxGateParts; ++s) pv[s] = s < n_parts ? src[s * part_stride] : 0.f;
-      v = pv[0];
-#pragma unroll
-      for (int s = 1; s < kMaxGateParts; ++s)
-        if (s < n_parts) v += pv[s];
-      if (bias != nullptr) v += bias[e];
-    }
-    xv[q] = v;
-  }
-  const float mx = row16_max(fmaxf(fmaxf(xv[0], xv[1]), fmaxf(xv[2], xv[3])));
-  float ex[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) ex[q] = taken[q] ? 0.f : expf(xv[q] - mx);
-  const float sum = row16_sum((ex[0] + ex[1]) + (ex[2] + ex[3]));
-  int my_e = -1;       // this lane's pick: k = j (lanes j < K)
-  float my_w = 0.f;
   // waves whose four rows are all past T skip the selection
   const bool wave_active = t0 + kTokPerWave * wave < T;
-  for (int k = 0; k < K && wave_active; ++k) {
-    // local best untaken (NaN counts as -inf; ties -> lower expert index)
-    float bv = -INFINITY;
-    int bi = 64;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float v = xv[q] == xv[q] ? xv[q] : -INFINITY;
-      if (!taken[q] && (v > bv || bi == 64)) {
-        bv = v;
-        bi = j + 16 * q;
-      }
-    }
-    const float m = row16_max(bv);
-    const int win = row16_min((bi < 64 && bv == m) ? bi : 64);
-    // probability of the winner, from its owner lane (j = win % 16)
-    float pw = 0.f;
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      if (j + 16 * q == win) {
-        taken[q] = true;
-        pw = ex[q] / sum;
-      }
-    pw = __shfl(pw, (lane & ~15) + (win & 15), 64);
-    if (j == k) {
-      my_e = win;
-      my_w = pw;
-    }
-  }
+  int my_e;
+  float my_w;
+  route_token(logits, ld, n_parts, part_stride, bias, t, active, wave_active, E, K, lane, my_e,
+              my_w);
   if (active && j < K) {
     topk_idx[(int64_t)t * K + j] = my_e;
     topk_w[(int64_t)t * K + j] = my_w;

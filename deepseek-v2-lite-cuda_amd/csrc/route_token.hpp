@@ -1,0 +1,87 @@
+// Softmax and top-K selection of one token on a 16-lane row, shared by the
+// route kernel (moe_route.hip) and the small-group GEMM that routes a decode
+// step in its prologue (gemm.hip), so both pick the same experts with the same
+// weights, bit for bit.
+#pragma once
+
+#include <math.h>
+
+#include "dsk_common.hpp"
+
+namespace dsk {
+
+constexpr int kMaxGateParts = 16;  // partial gate-sum planes a logit may be split into
+
+// Token t on one 16-lane row: lane j of the row holds the logits of experts j,
+// j+16, j+32, j+48, so every reduction is a 4-value local step plus a 16-lane
+// DPP step. The logits are the sum of n_parts partial planes (K slices of the
+// gate GEMM) in plane order, plus the optional per-expert bias. Lane j < K of
+// the row gets the j-th pick (my_e, my_w: expert and softmax probability,
+// descending, NaN as -inf, ties to the lower index). active: t < T (uniform
+// over the row); wave_active: some row of the wave is active (the selection
+// loop has wave-wide DPP steps).
+__device__ __forceinline__ void route_token(const float* __restrict__ logits, int64_t ld,
+                                            int n_parts, int64_t part_stride,
+                                            const float* __restrict__ bias, int t, bool active,
+                                            bool wave_active, int E, int K, int lane, int& my_e,
+                                            float& my_w) {
+  const int j = lane & 15;
+  float xv[4];
+  bool taken[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int e = j + 16 * q;
+    taken[q] = e >= E;  // padding experts are never chosen
+    float v = -INFINITY;
+    if (active && e < E) {
+      // all plane loads issued first, then summed in plane order
+      const float* src = logits + (int64_t)t * ld + e;
+      float pv[kMaxGateParts];
+#pragma unroll
+      for (int s = 0; s < kMaxGateParts; ++s) pv[s] = s < n_parts ? src[s * part_stride] : 0.f;
+      v = pv[0];
+#pragma unroll
+      for (int s = 1; s < kMaxGateParts; ++s)
+        if (s < n_parts) v += pv[s];
+      if (bias != nullptr) v += bias[e];
+    }
+    xv[q] = v;
+  }
+  const float mx = row16_max(fmaxf(fmaxf(xv[0], xv[1]), fmaxf(xv[2], xv[3])));
+  float ex[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) ex[q] = taken[q] ? 0.f : expf(xv[q] - mx);
+  const float sum = row16_sum((ex[0] + ex[1]) + (ex[2] + ex[3]));
+  my_e = -1;
+  my_w = 0.f;
+  for (int k = 0; k < K && wave_active; ++k) {
+    // local best untaken (NaN counts as -inf; ties -> lower expert index)
+    float bv = -INFINITY;
+    int bi = 64;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float v = xv[q] == xv[q] ? xv[q] : -INFINITY;
+      if (!taken[q] && (v > bv || bi == 64)) {
+        bv = v;
+        bi = j + 16 * q;
+      }
+    }
+    const float m = row16_max(bv);
+    const int win = row16_min((bi < 64 && bv == m) ? bi : 64);
+    // probability of the winner, from its owner lane (j = win % 16)
+    float pw = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (j + 16 * q == win) {
+        taken[q] = true;
+        pw = ex[q] / sum;
+      }
+    pw = __shfl(pw, (lane & ~15) + (win & 15), 64);
+    if (j == k) {
+      my_e = win;
+      my_w = pw;
+    }
+  }
+}
+
+}  // namespace dsk
