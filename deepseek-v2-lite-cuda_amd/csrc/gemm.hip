@@ -1510,8 +1510,8 @@ static int run_gemm_t(const GemmArgs& a, hipStream_t st) {
   // fragment-tiled weights with K % 128 == 0 and 16-byte aligned output rows:
   // one wave per SIMD, weights straight to registers. Measured on MI355X at
   // T=4096: 234 us against 251 us for the down projection, but 448 against
-  // 418 us for the gathered SwiGLU projection, which stays on the 8-wave
-  // kernel.
+  // 418 us for the gathered SwiGLU projection (368 against 360 us in steady
+  // state), which stays on the 8-wave kernel.
   if (DSK_GEMM_WIDE && TILED && !(SWIGLU && GATHER) && a.K % (2 * kWideBK) == 0 &&
       aligned16(a.C) && a.ldc % 8 == 0)
     return launch_wide_gemm<SWIGLU, GATHER>(a, st);
