@@ -1503,6 +1503,11 @@ template <bool SWIGLU, bool GATHER, bool TILED>
 static int run_gemm_t(const GemmArgs& a, hipStream_t st) {
   // groups of at most 64 rows (decode): weight streaming kernel
   const int rows = a.max_group_rows > 0 ? std::min(a.max_group_rows, a.M) : a.M;
+  // routing in the prologue exists only in the small-group SwiGLU kernel with gathered rows
+  DSK_REQUIRE(a.rt_parts == nullptr ||
+                  (SWIGLU && GATHER && rows <= kSkinnyMaxRows && a.offsets != nullptr &&
+                   a.rt_T >= 1 && a.rt_T <= kRouteInGemmTokens && a.M <= kRouteInGemmSlots),
+              DSK_ERR_INVALID_ARG, "grouped GEMM: routing in the prologue needs a small SwiGLU step");
   if (rows <= kSkinnyMaxRows) return launch_skinny<SWIGLU, GATHER, TILED>(a, rows, st);
 #ifndef DSK_GEMM_WIDE
 #define DSK_GEMM_WIDE 1
