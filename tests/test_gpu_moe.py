@@ -377,6 +377,42 @@ def test_layer_forward_with_gate_matches_oracle(dsk, full_layer, tiled_layer, T,
     assert torch.equal(out, out2)
 
 
+@pytest.mark.parametrize("case", ["random", "zipf", "all_tied", "neg_inf"])
+def test_single_token_routing_in_gemm_matches_route_kernel(dsk, full_layer, tiled_layer, case):
+    """At T = 1 the fused layer routes inside GEMM1's prologue (no route launch).
+    Its routing outputs must be the route kernel's (moe_routing on the same
+    logits) bit for bit: expert indices and order, weights, offsets (the scan of
+    the counts); ties go to the lower index and -inf experts are never picked
+    while finite ones remain."""
+    from ds_kernels import synthetic as syn
+    W, w1, w2, nsh, Wn = full_layer
+    w1, w2 = tiled_layer
+    g = torch.Generator().manual_seed(7)
+    if case == "all_tied":
+        logits = torch.zeros(1, 64)
+    else:
+        logits = torch.randn(1, 64, generator=g)
+        if case == "zipf":
+            logits = logits + syn.zipf_router_bias()
+        if case == "neg_inf":
+            logits[0, ::3] = -float("inf")
+    logits = logits.float().contiguous().to(DEV)
+    x = syn.tokens(1).to(torch.bfloat16).to(DEV)
+    out, (idx, w, off) = dsk.moe_fused_forward_logits(logits, x, w1, w2, 6, nsh, 64,
+                                                      return_routing=True)
+    ridx, rw, rcounts = dsk.moe_routing(logits, 6)
+    assert torch.equal(idx, ridx)
+    assert torch.equal(w, rw)
+    assert torch.equal(off, dsk.moe_scan(rcounts))
+    if case == "all_tied":
+        assert idx.cpu().tolist() == [[0, 1, 2, 3, 4, 5]]
+    if case == "neg_inf":
+        assert all(int(e) % 3 != 0 for e in idx.cpu().ravel())
+    lg = logits.cpu().numpy()
+    ref = _oracle_layer(Wn, x.cpu(), lg, 6)
+    assert max_rel_err(np32(out), ref) <= BF16_TOL
+
+
 @pytest.mark.parametrize("T", [16, 300])
 def test_layer_forward_graph_replay_matches_eager(dsk, full_layer, tiled_layer, T):
     """The layer captured in a HIP graph (T=16: single routing launch and the
