@@ -267,9 +267,11 @@ int dsk_linear_split(const dsk_bf16* x, int64_t ld_x, const dsk_bf16* w_tiled,
  * out[b][m][n] = sum_k x[b][m][k] * w[b][n][k] for M <= 4 token rows, with w
  * fragment-tiled [batch, N/32, K/16, 64, 8] (K % 128 == 0, N % 32 == 0), fp32
  * sums rounded once to bf16. Entry b of x starts x_batch_stride elements
- * after entry b-1, rows ld_x apart; outputs n < n_split go to out0 (row pitch
- * ld_out0, entry stride out0_batch_stride), the others to out1 at column
- * n - n_split (n_split = N: out1 unused). Vector-ALU dot products over 8 weight
+ * after entry b-1, rows ld_x apart; entry b of w starts w_batch_stride
+ * elements after entry b-1 (0: one weight for every entry); outputs
+ * n < n_split go to out0 (row pitch ld_out0, entry stride out0_batch_stride),
+ * the others to out1 at column n - n_split (n_split = N: out1 unused).
+ * Vector-ALU dot products over 8 weight
  * rows per lane group, so a one-token projection of N rows runs as N/8 lane
  * groups instead of N/32 workgroups: the q/kv_a, per-head and o projections of
  * a one-token absorbed-MLA decode step. The reference has no counterpart (it
