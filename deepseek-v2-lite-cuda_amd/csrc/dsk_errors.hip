@@ -26,4 +26,4 @@ int check_launch(const char* what) {
 
 extern "C" const char* dsk_last_error(void) { return dsk::g_last_error.c_str(); }
 
-extern "C" int dsk_abi_version(void) { return 2; }
+extern "C" int dsk_abi_version(void) { return 3; }

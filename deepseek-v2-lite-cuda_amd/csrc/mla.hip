@@ -307,21 +307,61 @@ static int check_rope(const void* x, int64_t sb, int64_t sh, int64_t ss, const v
 // eager sequence (mla.py:366-381) in one pass, p = softmax over keys of
 // bf16(score * scale) + mask, in fp32, rounded once to bf16. The scaled score
 // is rounded to bf16 first because the reference multiplies the bf16 matmul
-// output by the scale in the model dtype. With causal masking, key j of query
-// i (query positions are the last q_len of the kv_len keys) is masked for
-// j > i + kv_len - q_len: its probability is 0 and its score is never read.
+// output by the scale in the model dtype.
+// * Causal: key j of query i (query positions are the last q_len of the kv_len
+//   keys) is masked for j > i + kv_len - q_len: its probability is 0 and its
+//   score is never read.
+// * Additive mask (mla.py:374, `attn_weights + attention_mask`): element j of the
+//   row's mask row is added to the scaled score. The sum takes the dtype torch
+//   promotes to: a bf16 mask gives a bf16 sum (rounded), an fp32 mask an fp32
+//   sum. Mask rows are addressed by (batch, head, query) strides, so a
+//   [b, 1, q, kv] mask broadcasts over the heads with a head stride of 0.
+// * Keys from kv_len up to the row's next multiple of 8 are written as 0, so a
+//   score buffer padded to 16-byte rows feeds the P.V product with exact zeros.
+struct SoftmaxMask {
+  const void* ptr;  // nullptr: no additive mask
+  int f32;          // 1: fp32 elements, 0: bf16
+  int heads;        // rows are (batch, head, query) with query fastest
+  int64_t sb, sh, sq;  // element strides; key stride 1
+};
+
+__device__ __forceinline__ float mask_at(const SoftmaxMask& m, int64_t off) {
+  return m.f32 ? reinterpret_cast<const float*>(m.ptr)[off]
+               : bf16_to_f32(reinterpret_cast<const uint16_t*>(m.ptr)[off]);
+}
+
+// The scaled (and masked) score of key `col + e` from the loaded chunk w.
+__device__ __forceinline__ float softmax_logit(uint32_t word, int e, float scale, const SoftmaxMask& m,
+                                               int64_t moff, int col, int kv_len) {
+  const float x = (e & 1) ? bf16hi(word) : bf16lo(word);
+  float xs = bf16_to_f32(f32_to_bf16(x * scale));
+  if (m.ptr != nullptr && col + e < kv_len) {
+    const float mv = mask_at(m, moff + col + e);
+    xs = m.f32 ? xs + mv : bf16_to_f32(f32_to_bf16(xs + mv));
+  }
+  return xs;
+}
+
+__device__ __forceinline__ int64_t softmax_mask_row(const SoftmaxMask& m, int64_t row, int q_len) {
+  if (m.ptr == nullptr) return 0;
+  const int64_t qi = row % q_len, bh = row / q_len;
+  return (bh / m.heads) * m.sb + (bh % m.heads) * m.sh + qi * m.sq;
+}
+
 // One wave per row; a lane holds 8 consecutive keys of each 512-key chunk in
 // registers (kv_len <= 512 * NC).
 template <int NC>
 __global__ __launch_bounds__(256) void attn_softmax_kernel(uint16_t* __restrict__ sc, int64_t ld,
                                                            int64_t rows, int kv_len, int q_len,
-                                                           float scale, int causal) {
+                                                           float scale, int causal,
+                                                           SoftmaxMask mask) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;  // uniform over the wave
   uint16_t* p = sc + row * ld;
   const int qi = (int)(row % q_len);
   const int limit = causal ? min(kv_len, qi + 1 + (kv_len - q_len)) : kv_len;
+  const int64_t moff = softmax_mask_row(mask, row, q_len);
   float v[NC][8];
   float mx = -INFINITY;
 #pragma unroll
@@ -331,9 +371,8 @@ __global__ __launch_bounds__(256) void attn_softmax_kernel(uint16_t* __restrict_
     if (col < limit) w = *reinterpret_cast<const u32x4_t*>(p + col);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float x = (e & 1) ? bf16hi(w[e / 2]) : bf16lo(w[e / 2]);
-      const float xs = bf16_to_f32(f32_to_bf16(x * scale));
-      v[c][e] = col + e < limit ? xs : -INFINITY;
+      v[c][e] = col + e < limit ? softmax_logit(w[e / 2], e, scale, mask, moff, col, kv_len)
+                                : -INFINITY;
       mx = fmaxf(mx, v[c][e]);
     }
   }
@@ -359,6 +398,62 @@ __global__ __launch_bounds__(256) void attn_softmax_kernel(uint16_t* __restrict_
       for (int e = 0; e < 4; ++e) o[e] = pack_bf16x2(v[c][2 * e] * inv, v[c][2 * e + 1] * inv);
       *reinterpret_cast<u32x4_t*>(p + col) = o;
     }
+  }
+}
+
+// Rows longer than the register-resident kernel holds (kv_len > 4096): one wave
+// per row in two passes over 512-key chunks. The first keeps a running max and
+// sum per lane (each lane's sum rescaled when its max grows), combined over the
+// wave; the second recomputes the logits and writes exp(x - max) / sum. The
+// probabilities are the single-pass kernel's formula with the sum accumulated
+// in a different order.
+__global__ __launch_bounds__(256) void attn_softmax_long_kernel(uint16_t* __restrict__ sc,
+                                                                int64_t ld, int64_t rows,
+                                                                int kv_len, int q_len, float scale,
+                                                                int causal, SoftmaxMask mask) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;  // uniform over the wave
+  uint16_t* p = sc + row * ld;
+  const int qi = (int)(row % q_len);
+  const int limit = causal ? min(kv_len, qi + 1 + (kv_len - q_len)) : kv_len;
+  const int64_t moff = softmax_mask_row(mask, row, q_len);
+  float m = -INFINITY, s = 0.f;
+  for (int col = lane * 8; col < limit; col += 512) {
+    const u32x4_t w = *reinterpret_cast<const u32x4_t*>(p + col);
+    float x[8];
+    float cm = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      x[e] = col + e < limit ? softmax_logit(w[e / 2], e, scale, mask, moff, col, kv_len)
+                             : -INFINITY;
+      cm = fmaxf(cm, x[e]);
+    }
+    if (cm == -INFINITY) continue;
+    if (cm > m) {
+      s = m == -INFINITY ? 0.f : s * __expf(m - cm);
+      m = cm;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += x[e] == -INFINITY ? 0.f : __expf(x[e] - m);
+  }
+  const float mx = wave_max(m);
+  const float sum = wave_sum(m == -INFINITY ? 0.f : s * __expf(m - mx));
+  const float inv = 1.f / sum;
+  for (int col = lane * 8; col < kv_len; col += 512) {
+    u32x4_t w = u32x4_t{0u, 0u, 0u, 0u};
+    if (col < limit) w = *reinterpret_cast<const u32x4_t*>(p + col);
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x = col + e < limit ? softmax_logit(w[e / 2], e, scale, mask, moff, col, kv_len)
+                                      : -INFINITY;
+      y[e] = (x == -INFINITY ? 0.f : __expf(x - mx)) * inv;  // a fully masked row gives NaN, as torch
+    }
+    u32x4_t o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = pack_bf16x2(y[2 * e], y[2 * e + 1]);
+    *reinterpret_cast<u32x4_t*>(p + col) = o;
   }
 }
 
@@ -466,16 +561,19 @@ __global__ __launch_bounds__(kPackThreads) void attn_pack_kernel(
     const uint16_t* __restrict__ q, int64_t ld_q, const uint16_t* __restrict__ kv,
     int64_t ld_kv, const uint16_t* __restrict__ kpe, int64_t ld_kpe,
     const uint16_t* __restrict__ cos_t, const uint16_t* __restrict__ sin_t, int64_t ld_cs,
-    uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_t, uint16_t* __restrict__ v_out,
-    int S, int heads) {
+    int64_t cs_bs, uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_t,
+    uint16_t* __restrict__ v_out, int S, int SP, int heads) {
   __shared__ u32x4_t tile[kPackPos * kPackChunks];  // K rows of the block, 24 KB
   const int tid = threadIdx.x;
   const int pos0 = blockIdx.x * kPackPos;
   const int hh = blockIdx.y;
   const int bi = blockIdx.z;
-  const int npos = min(kPackPos, S - pos0);
+  const int npos = min(kPackPos, S - pos0);   // real positions of the block
+  const int nall = min(kPackPos, SP - pos0);  // with the zero padding up to SP
   const int64_t bh = (int64_t)bi * heads + hh;
   const int64_t row0 = (int64_t)bi * S + pos0;  // token row of the block's first position
+  cos_t += bi * cs_bs;
+  sin_t += bi * cs_bs;
 
   // q nope -> Q, v -> V, k nope -> tile: 16 chunks per position each
 #pragma unroll
@@ -489,8 +587,13 @@ __global__ __launch_bounds__(kPackThreads) void attn_pack_kernel(
       const u32x4_t kn = *reinterpret_cast<const u32x4_t*>(kvr + 8 * c);
       const u32x4_t vv = *reinterpret_cast<const u32x4_t*>(kvr + kPackNope + 8 * c);
       *reinterpret_cast<u32x4_t*>(q_out + (bh * S + pos0 + p) * kPackQK + 8 * c) = qn;
-      *reinterpret_cast<u32x4_t*>(v_out + (bh * S + pos0 + p) * kPackV + 8 * c) = vv;
+      *reinterpret_cast<u32x4_t*>(v_out + (bh * SP + pos0 + p) * kPackV + 8 * c) = vv;
       tile[pack_slot(p, c)] = kn;
+    } else if (p < nall) {  // padding position: zero V row and K column
+      const u32x4_t z = u32x4_t{0u, 0u, 0u, 0u};
+      *reinterpret_cast<u32x4_t*>(v_out + (bh * SP + pos0 + p) * kPackV + 8 * c) = z;
+      tile[pack_slot(p, c)] = z;
+      if (c < kPackChunks - 16) tile[pack_slot(p, 16 + c)] = z;
     }
   }
   // rotation, 8 pairs per item: q_pe into Q, k_pe into the tile
@@ -541,12 +644,12 @@ __global__ __launch_bounds__(kPackThreads) void attn_pack_kernel(
   // K^T: rows 2dp and 2dp + 1, 8 positions (octet po) per item; 8 consecutive
   // lanes cover one 128-byte row segment of each
   const uint32_t* tw = reinterpret_cast<const uint32_t*>(tile);
-  uint16_t* kt_bh = k_t + bh * kPackQK * S + pos0;
+  uint16_t* kt_bh = k_t + bh * kPackQK * SP + pos0;
 #pragma unroll
   for (int r = 0; r < (kPackQK / 2) * 8 / kPackThreads; ++r) {
     const int it = tid + kPackThreads * r;
     const int po = it & 7, dp = it >> 3;
-    if (8 * po < npos) {
+    if (8 * po < nall) {
       uint32_t w[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) w[i] = tw[pack_slot(8 * po + i, dp >> 2) * 4 + (dp & 3)];
@@ -556,10 +659,47 @@ __global__ __launch_bounds__(kPackThreads) void attn_pack_kernel(
         lo[k] = __builtin_amdgcn_perm(w[2 * k + 1], w[2 * k], 0x05040100u);
         hi[k] = __builtin_amdgcn_perm(w[2 * k + 1], w[2 * k], 0x07060302u);
       }
-      *reinterpret_cast<u32x4_t*>(kt_bh + (int64_t)(2 * dp) * S + 8 * po) = lo;
-      *reinterpret_cast<u32x4_t*>(kt_bh + (int64_t)(2 * dp + 1) * S + 8 * po) = hi;
+      *reinterpret_cast<u32x4_t*>(kt_bh + (int64_t)(2 * dp) * SP + 8 * po) = lo;
+      *reinterpret_cast<u32x4_t*>(kt_bh + (int64_t)(2 * dp + 1) * SP + 8 * po) = hi;
     }
   }
+}
+
+extern "C" int dsk_mla_attn_pack_ex(const dsk_bf16* q, int64_t ld_q, const dsk_bf16* kv,
+                                    int64_t ld_kv, const dsk_bf16* k_pe, int64_t ld_kpe,
+                                    const dsk_bf16* cos_t, const dsk_bf16* sin_t, int64_t ld_cs,
+                                    int64_t cs_batch_stride, dsk_bf16* q_out, dsk_bf16* k_t,
+                                    dsk_bf16* v_out, int batch, int seq, int seq_pad, int heads,
+                                    int nope, int rope, int v_dim, void* stream) {
+  DSK_REQUIRE(nope == kPackNope && rope == kPackRope && v_dim == kPackV, DSK_ERR_INVALID_ARG,
+              "attn_pack: head dims must be nope 128, rope 64, v 128");
+  DSK_REQUIRE(batch >= 0 && seq >= 0 && heads >= 0, DSK_ERR_INVALID_ARG,
+              "attn_pack: negative size");
+  if ((int64_t)batch * seq * heads == 0) return DSK_OK;
+  DSK_REQUIRE(seq_pad % 8 == 0 && seq_pad >= seq && seq_pad - seq < 8, DSK_ERR_INVALID_ARG,
+              "attn_pack: seq_pad must be seq rounded up to a multiple of 8");
+  DSK_REQUIRE(batch <= 65535 && heads <= 65535, DSK_ERR_INVALID_ARG,
+              "attn_pack: batch and heads must be at most 65535");
+  DSK_REQUIRE(q && kv && k_pe && cos_t && sin_t && q_out && k_t && v_out, DSK_ERR_NULL_PTR,
+              "attn_pack: NULL pointer");
+  DSK_REQUIRE(aligned16(q) && aligned16(kv) && aligned16(k_pe) && aligned16(cos_t) &&
+                  aligned16(sin_t) && aligned16(q_out) && aligned16(k_t) && aligned16(v_out) &&
+                  ld_q % 8 == 0 && ld_kv % 8 == 0 && ld_kpe % 8 == 0 && ld_cs % 8 == 0 &&
+                  cs_batch_stride % 8 == 0,
+              DSK_ERR_ALIGNMENT, "attn_pack: rows must be 16-byte aligned");
+  DSK_REQUIRE(ld_q >= (int64_t)heads * kPackQK && ld_kv >= (int64_t)heads * (kPackNope + kPackV) &&
+                  ld_kpe >= kPackRope && ld_cs >= kPackRope && cs_batch_stride >= 0,
+              DSK_ERR_INVALID_ARG, "attn_pack: row stride smaller than the row");
+  const dim3 grid((unsigned)((seq + kPackPos - 1) / kPackPos), (unsigned)heads, (unsigned)batch);
+  hipLaunchKernelGGL(attn_pack_kernel, grid, dim3(kPackThreads), 0, as_stream(stream),
+                     reinterpret_cast<const uint16_t*>(q), ld_q,
+                     reinterpret_cast<const uint16_t*>(kv), ld_kv,
+                     reinterpret_cast<const uint16_t*>(k_pe), ld_kpe,
+                     reinterpret_cast<const uint16_t*>(cos_t),
+                     reinterpret_cast<const uint16_t*>(sin_t), ld_cs, cs_batch_stride,
+                     reinterpret_cast<uint16_t*>(q_out), reinterpret_cast<uint16_t*>(k_t),
+                     reinterpret_cast<uint16_t*>(v_out), seq, seq_pad, heads);
+  return check_launch("attn_pack_kernel");
 }
 
 extern "C" int dsk_mla_attn_pack(const dsk_bf16* q, int64_t ld_q, const dsk_bf16* kv,
@@ -568,61 +708,63 @@ extern "C" int dsk_mla_attn_pack(const dsk_bf16* q, int64_t ld_q, const dsk_bf16
                                  dsk_bf16* q_out, dsk_bf16* k_t, dsk_bf16* v_out, int batch,
                                  int seq, int heads, int nope, int rope, int v_dim,
                                  void* stream) {
-  DSK_REQUIRE(nope == kPackNope && rope == kPackRope && v_dim == kPackV, DSK_ERR_INVALID_ARG,
-              "attn_pack: head dims must be nope 128, rope 64, v 128");
-  DSK_REQUIRE(batch >= 0 && seq >= 0 && heads >= 0, DSK_ERR_INVALID_ARG,
-              "attn_pack: negative size");
-  if ((int64_t)batch * seq * heads == 0) return DSK_OK;
-  DSK_REQUIRE(seq % 8 == 0, DSK_ERR_INVALID_ARG, "attn_pack: seq must be a multiple of 8");
-  DSK_REQUIRE(batch <= 65535 && heads <= 65535, DSK_ERR_INVALID_ARG,
-              "attn_pack: batch and heads must be at most 65535");
-  DSK_REQUIRE(q && kv && k_pe && cos_t && sin_t && q_out && k_t && v_out, DSK_ERR_NULL_PTR,
-              "attn_pack: NULL pointer");
-  DSK_REQUIRE(aligned16(q) && aligned16(kv) && aligned16(k_pe) && aligned16(cos_t) &&
-                  aligned16(sin_t) && aligned16(q_out) && aligned16(k_t) && aligned16(v_out) &&
-                  ld_q % 8 == 0 && ld_kv % 8 == 0 && ld_kpe % 8 == 0 && ld_cs % 8 == 0,
-              DSK_ERR_ALIGNMENT, "attn_pack: rows must be 16-byte aligned");
-  DSK_REQUIRE(ld_q >= (int64_t)heads * kPackQK && ld_kv >= (int64_t)heads * (kPackNope + kPackV) &&
-                  ld_kpe >= kPackRope && ld_cs >= kPackRope,
-              DSK_ERR_INVALID_ARG, "attn_pack: row stride smaller than the row");
-  const dim3 grid((unsigned)((seq + kPackPos - 1) / kPackPos), (unsigned)heads, (unsigned)batch);
-  hipLaunchKernelGGL(attn_pack_kernel, grid, dim3(kPackThreads), 0, as_stream(stream),
-                     reinterpret_cast<const uint16_t*>(q), ld_q,
-                     reinterpret_cast<const uint16_t*>(kv), ld_kv,
-                     reinterpret_cast<const uint16_t*>(k_pe), ld_kpe,
-                     reinterpret_cast<const uint16_t*>(cos_t),
-                     reinterpret_cast<const uint16_t*>(sin_t), ld_cs,
-                     reinterpret_cast<uint16_t*>(q_out), reinterpret_cast<uint16_t*>(k_t),
-                     reinterpret_cast<uint16_t*>(v_out), seq, heads);
-  return check_launch("attn_pack_kernel");
+  DSK_REQUIRE(seq % 8 == 0, DSK_ERR_INVALID_ARG,
+              "attn_pack: seq must be a multiple of 8 (dsk_mla_attn_pack_ex pads other lengths)");
+  return dsk_mla_attn_pack_ex(q, ld_q, kv, ld_kv, k_pe, ld_kpe, cos_t, sin_t, ld_cs, 0, q_out,
+                              k_t, v_out, batch, seq, seq, heads, nope, rope, v_dim, stream);
 }
 
-extern "C" int dsk_attn_softmax(dsk_bf16* scores, int64_t ld, int64_t rows, int kv_len,
-                                int q_len, float scale, int causal, void* stream) {
+namespace {
+int attn_softmax_launch(dsk_bf16* scores, int64_t ld, int64_t rows, int kv_len, int q_len,
+                        float scale, int causal, const SoftmaxMask& mask, void* stream) {
   DSK_REQUIRE(rows >= 0 && kv_len > 0 && q_len > 0, DSK_ERR_INVALID_ARG,
               "attn_softmax: rows >= 0, kv_len > 0 and q_len > 0 required");
-  DSK_REQUIRE(kv_len % 8 == 0 && kv_len <= 4096, DSK_ERR_INVALID_ARG,
-              "attn_softmax: kv_len must be a multiple of 8 and at most 4096");
   DSK_REQUIRE(rows % q_len == 0 && (!causal || q_len <= kv_len), DSK_ERR_INVALID_ARG,
               "attn_softmax: rows must be a multiple of q_len, and q_len <= kv_len when causal");
   if (rows == 0) return DSK_OK;
   DSK_REQUIRE(scores != nullptr, DSK_ERR_NULL_PTR, "attn_softmax: NULL pointer");
-  DSK_REQUIRE(aligned16(scores) && ld % 8 == 0 && ld >= kv_len, DSK_ERR_ALIGNMENT,
-              "attn_softmax: rows must be 16-byte aligned with ld >= kv_len");
+  DSK_REQUIRE(aligned16(scores) && ld % 8 == 0 && ld >= (int64_t)align_up((size_t)kv_len, 8),
+              DSK_ERR_ALIGNMENT,
+              "attn_softmax: rows must be 16-byte aligned with ld >= kv_len rounded up to 8");
   const unsigned grid = (unsigned)((rows + 3) / 4);
   uint16_t* s = reinterpret_cast<uint16_t*>(scores);
   hipStream_t st = as_stream(stream);
   if (kv_len <= 512)
     hipLaunchKernelGGL(attn_softmax_kernel<1>, dim3(grid), dim3(256), 0, st, s, ld, rows, kv_len,
-                       q_len, scale, causal);
+                       q_len, scale, causal, mask);
   else if (kv_len <= 1024)
     hipLaunchKernelGGL(attn_softmax_kernel<2>, dim3(grid), dim3(256), 0, st, s, ld, rows, kv_len,
-                       q_len, scale, causal);
+                       q_len, scale, causal, mask);
   else if (kv_len <= 2048)
     hipLaunchKernelGGL(attn_softmax_kernel<4>, dim3(grid), dim3(256), 0, st, s, ld, rows, kv_len,
-                       q_len, scale, causal);
-  else
+                       q_len, scale, causal, mask);
+  else if (kv_len <= 4096)
     hipLaunchKernelGGL(attn_softmax_kernel<8>, dim3(grid), dim3(256), 0, st, s, ld, rows, kv_len,
-                       q_len, scale, causal);
+                       q_len, scale, causal, mask);
+  else
+    hipLaunchKernelGGL(attn_softmax_long_kernel, dim3(grid), dim3(256), 0, st, s, ld, rows,
+                       kv_len, q_len, scale, causal, mask);
   return check_launch("attn_softmax_kernel");
+}
+}  // namespace
+
+extern "C" int dsk_attn_softmax(dsk_bf16* scores, int64_t ld, int64_t rows, int kv_len,
+                                int q_len, float scale, int causal, void* stream) {
+  return attn_softmax_launch(scores, ld, rows, kv_len, q_len, scale, causal,
+                             SoftmaxMask{nullptr, 0, 1, 0, 0, 0}, stream);
+}
+
+extern "C" int dsk_attn_softmax_masked(dsk_bf16* scores, int64_t ld, int64_t rows, int kv_len,
+                                       int q_len, int heads, float scale, int causal,
+                                       const void* mask, int mask_dtype, int64_t mask_sb,
+                                       int64_t mask_sh, int64_t mask_sq, void* stream) {
+  DSK_REQUIRE(mask_dtype == DSK_DTYPE_BF16 || mask_dtype == DSK_DTYPE_F32, DSK_ERR_INVALID_ARG,
+              "attn_softmax: mask dtype must be DSK_DTYPE_BF16 or DSK_DTYPE_F32");
+  DSK_REQUIRE(heads > 0 && (rows / (q_len > 0 ? q_len : 1)) % heads == 0, DSK_ERR_INVALID_ARG,
+              "attn_softmax: rows / q_len must be a multiple of heads");
+  DSK_REQUIRE(mask != nullptr || rows == 0, DSK_ERR_NULL_PTR, "attn_softmax: NULL mask");
+  return attn_softmax_launch(scores, ld, rows, kv_len, q_len, scale, causal,
+                             SoftmaxMask{mask, mask_dtype == DSK_DTYPE_F32 ? 1 : 0, heads,
+                                         mask_sb, mask_sh, mask_sq},
+                             stream);
 }

@@ -43,8 +43,12 @@ SIGNATURES = {
     "dsk_linear_rowsq": (_I, [_P, _I64, _P, _P, _I64, _I, _I, _I, _P, _I64, _I, _I, _P]),
     "dsk_linear_rowscale": (_I, [_P, _I64, _P, _P, _I64, _I, _I, _I, _P, _I64, _I, _I, _F, _P]),
     "dsk_attn_softmax": (_I, [_P, _I64, _I64, _I, _I, _F, _I, _P]),
+    "dsk_attn_softmax_masked": (_I, [_P, _I64, _I64, _I, _I, _I, _F, _I, _P, _I, _I64, _I64,
+                                     _I64, _P]),
     "dsk_mla_attn_pack": (_I, [_P, _I64, _P, _I64, _P, _I64, _P, _P, _I64, _P, _P, _P, _I, _I,
                                _I, _I, _I, _I, _P]),
+    "dsk_mla_attn_pack_ex": (_I, [_P, _I64, _P, _I64, _P, _I64, _P, _P, _I64, _I64, _P, _P, _P,
+                                  _I, _I, _I, _I, _I, _I, _I, _P]),
     "dsk_linear_batched": (_I, [_P, _I64, _I64, _P, _P, _I64, _I64, _I, _I, _I, _I, _P]),
     "dsk_linear_rows": (_I, [_P, _I64, _I64, _P, _I64, _P, _I64, _I64, _P, _I64, _I64, _I, _I, _I,
                              _I, _I, _P]),

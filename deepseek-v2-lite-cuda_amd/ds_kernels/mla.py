@@ -144,7 +144,8 @@ def _projection_rows(x: torch.Tensor, W: MLAWeights, eps: float, with_latent: bo
 def mla_projections(x: torch.Tensor, W: MLAWeights, cos: torch.Tensor, sin: torch.Tensor,
                     eps: float = 1e-6, with_latent: bool = True):
     """The projection block of DeepSeekMLA.forward (mla.py:318-352, BASELINE
-    config 3). x: bf16 [b, s, H]; cos/sin: bf16 [s, rope_dim] for positions 0..s-1.
+    config 3). x: bf16 [b, s, H]; cos/sin: [>= s, rope_dim] for positions 0..s-1,
+    or [b, s, rope_dim] per batch entry (tables indexed by position_ids).
     Returns (q_nope [b,h,s,nope], q_rot [b,h,s,r], k_nope [b,h,s,nope],
     v [b,h,s,v], k_rot [b,1,s,r], latent_normed [b,s,kv_lora]); q_nope, k_nope
     and v are strided views of the projection outputs.
@@ -162,42 +163,81 @@ def mla_projections(x: torch.Tensor, W: MLAWeights, cos: torch.Tensor, sin: torc
     q = q.view(b, s, h, nope + r).transpose(1, 2)                      # [b,h,s,192] view
     kv = kv.view(b, s, h, nope + vd).transpose(1, 2)
     k_pe = kva[..., lora:].view(b, s, 1, r).transpose(1, 2)           # [b,1,s,64] view
-    cb = cos.to(torch.bfloat16)[None, None].expand(b, 1, s, r)         # batch stride 0
-    sb = sin.to(torch.bfloat16)[None, None].expand(b, 1, s, r)
+    if cos.dim() == 3:        # per batch entry (tables indexed by position_ids)
+        cb = cos.to(torch.bfloat16)[:, None, :s]
+        sb = sin.to(torch.bfloat16)[:, None, :s]
+    else:                     # shared by the batch: batch stride 0
+        cb = cos[:s].to(torch.bfloat16)[None, None].expand(b, 1, s, r)
+        sb = sin[:s].to(torch.bfloat16)[None, None].expand(b, 1, s, r)
     q_rot, k_rot = ops.rope(q[..., nope:], k_pe, cb, sb)
     return q[..., :nope], q_rot, kv[..., :nope], kv[..., nope:], k_rot, latent
 
 
+def rope_tables_for(cos: torch.Tensor, sin: torch.Tensor, s: int,
+                    position_ids: Optional[torch.Tensor]):
+    """The tables apply_rotary_pos_emb uses (mla.py:186-187, 349-351): the
+    module's cos/sin cut to the sequence length, indexed by position_ids
+    [b, s] when given -> bf16 [s, d] (shared by the batch) or [b, s, d].
+    position_ids index the first s rows, as `cos[:q_len][position_ids]` does
+    in the reference; an index outside them raises IndexError here (torch
+    raises it there)."""
+    cs, sn = cos[:s].to(torch.bfloat16), sin[:s].to(torch.bfloat16)
+    if position_ids is None:
+        return cs, sn
+    pid = position_ids.to(device=cos.device, dtype=torch.long)
+    ops._req(pid.dim() == 2 and pid.shape[1] == s,
+             f"position_ids must be [bsz, {s}], got {tuple(position_ids.shape)}.")
+    if pid.numel() and bool(((pid < -s) | (pid >= s)).any()):
+        raise IndexError(f"position_ids must index the {s} table rows (positions -{s}..{s - 1}).")
+    return cs[pid].contiguous(), sn[pid].contiguous()
+
+
 def mla_forward(x: torch.Tensor, W: MLAWeights, cos: torch.Tensor, sin: torch.Tensor,
-                eps: float = 1e-6) -> torch.Tensor:
-    """DeepSeekMLA.forward (mla.py:295-393) for positions 0..s-1 with the causal
-    mask: projections on this package's kernels, o_proj on the MFMA GEMM, and
-    the attention core at the reference's precision (mla.py:366-384): bf16 Q.K^T
-    and .V in torch (right-hand operands made contiguous before the batched
-    products), the scale, causal mask, fp32 softmax and bf16 rounding in one
-    pass of attn_softmax_.
-    x: bf16 [b, s, H] -> bf16 [b, s, H], with s a multiple of 8 (the 16-byte
-    rows of the score and K^T buffers)."""
+                eps: float = 1e-6, attention_mask: Optional[torch.Tensor] = None,
+                position_ids: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """DeepSeekMLA.forward (mla.py:295-393): projections on this package's
+    kernels, o_proj on the MFMA GEMM, and the attention core at the
+    reference's precision (mla.py:366-384): bf16 Q.K^T and .V in torch
+    (right-hand operands contiguous), the scale, mask, fp32 softmax and bf16
+    rounding in one pass of attn_softmax_.
+    x: bf16 [b, s, H] -> bf16 [b, s, H], any s >= 1. cos/sin: the YaRN tables
+    for positions 0.. (at least s rows). attention_mask: additive [b, 1, s, s]
+    (bf16 or fp32, -inf where masked; anything broadcastable to it) used instead
+    of the causal mask, as in the reference; position_ids: [b, s] rows of the
+    tables for each token (default 0..s-1). With s % 8 != 0 the key dimension of
+    K^T, the scores and V is padded to a multiple of 8 with zeros."""
     b, s, H = x.shape
     h, nope, r = W.n_heads, W.nope, W.rope_dim
+    cs, sn = rope_tables_for(cos, sin, s, position_ids)
+    sp = (s + 7) // 8 * 8
     if (nope, r, W.v_dim) == (128, 64, 128):
         # Q, K^T and V packed head-major in one pass from the projection rows
         # (RoPE of q_pe and k_pe included); other head dims assemble them by copies
         qr, kv, kva, _ = _projection_rows(x, W, eps, with_latent=False)
-        q, kT, v = ops.mla_attn_pack(qr, kv, kva[..., W.kv_lora:], cos[:s], sin[:s], heads=h)
+        q, kT, v = ops.mla_attn_pack(qr, kv, kva[..., W.kv_lora:], cs, sn, heads=h, pad=True)
     else:
-        q_nope, q_rot, k_nope, v, k_rot, _ = mla_projections(x, W, cos, sin, eps,
-                                                             with_latent=False)
-        q = torch.cat([q_nope, q_rot], dim=-1)                         # [b,h,s,192]
-        kT = torch.empty((b, h, nope + r, s), dtype=torch.bfloat16, device=x.device)
-        kT[:, :, :nope].copy_(k_nope.transpose(-1, -2))
-        kT[:, :, nope:].copy_(k_rot.transpose(-1, -2).expand(b, h, r, s))
-        v = v.contiguous()
-    scores = torch.matmul(q, kT)                                       # bf16 [b,h,s,s]
-    p = ops.attn_softmax_(scores, W.softmax_scale, causal=True)       # scale, mask, softmax
+        q, kT, v = _assemble_attention_operands(x, W, cs, sn, eps, sp)
+    scores = torch.matmul(q, kT)                                       # bf16 [b,h,s,sp]
+    p = ops.attn_softmax_(scores, W.softmax_scale, causal=attention_mask is None, kv_len=s,
+                          mask=attention_mask)
     o = torch.matmul(p, v)                                             # [b,h,s,v]
     o = o.transpose(1, 2).reshape(b, s, W.n_heads * W.v_dim)
     return ops.linear(o, W.o)
+
+
+def _assemble_attention_operands(x, W: MLAWeights, cs, sn, eps, sp):
+    """Q [b,h,s,nope+r], K^T [b,h,nope+r,sp] and V [b,h,sp,v] by copies, for head
+    dims the pack kernel does not take; K^T columns and V rows past s are zero."""
+    b, s, _ = x.shape
+    h, nope, r = W.n_heads, W.nope, W.rope_dim
+    q_nope, q_rot, k_nope, v, k_rot, _ = mla_projections(x, W, cs, sn, eps, with_latent=False)
+    q = torch.cat([q_nope, q_rot], dim=-1)                             # [b,h,s,192]
+    kT = torch.zeros((b, h, nope + r, sp), dtype=torch.bfloat16, device=x.device)
+    kT[:, :, :nope, :s].copy_(k_nope.transpose(-1, -2))
+    kT[:, :, nope:, :s].copy_(k_rot.transpose(-1, -2).expand(b, h, r, s))
+    vp = torch.zeros((b, h, sp, W.v_dim), dtype=torch.bfloat16, device=x.device)
+    vp[:, :, :s].copy_(v)
+    return q, kT, vp
 
 
 # ------------------------------------------------------------ decoder layer --
@@ -230,13 +270,17 @@ class DecoderLayerWeights:
 
 
 def decoder_layer_forward(x: torch.Tensor, P: DecoderLayerWeights, cos: torch.Tensor,
-                          sin: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+                          sin: torch.Tensor, eps: float = 1e-6,
+                          attention_mask: Optional[torch.Tensor] = None,
+                          position_ids: Optional[torch.Tensor] = None) -> torch.Tensor:
     """DeepSeekDecoderLayer.forward (decoder_layer.py:108-139), BASELINE config 4:
-    RMSNorm -> MLA (causal) -> residual -> RMSNorm -> MoE (routed + shared) ->
-    residual. x: bf16 [b, s, H]."""
+    RMSNorm -> MLA -> residual -> RMSNorm -> MoE (routed + shared) -> residual.
+    x: bf16 [b, s, H]; attention_mask / position_ids as in mla_forward (causal
+    and positions 0..s-1 by default)."""
     b, s, H = x.shape
     h = ops.rms_norm(x, P.in_norm, eps)
-    x = x + mla_forward(h, P.mla, cos, sin, eps)
+    x = x + mla_forward(h, P.mla, cos, sin, eps, attention_mask=attention_mask,
+                        position_ids=position_ids)
     h = ops.rms_norm(x, P.post_norm, eps)
     m = moe_layer_forward(h.reshape(-1, H), P.gate, P.w1, P.w2, P.top_k, P.n_shared_groups)
     return x + m.view(b, s, H)

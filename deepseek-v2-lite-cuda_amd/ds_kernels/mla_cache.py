@@ -203,10 +203,17 @@ def _attend_up_projected(q: torch.Tensor, cache: LatentKVCache, W: MLAWeights, c
     cache.k_rope[:, :L].copy_(k_rot[:, 0])       # every cached key rotated once
     cache._rope_len = L
     qf = torch.cat([q[..., :nope].transpose(1, 2), q_rot], dim=-1)       # [b, h, n, 192]
-    kf = torch.cat([kv[..., :nope], k_rot.expand(b, h, L, r)], dim=-1)   # [b, h, L, 192]
-    scores = torch.matmul(qf, kf.transpose(-1, -2).contiguous())         # bf16 [b, h, n, L]
-    p = ops.attn_softmax_(scores, W.softmax_scale, causal=True)
-    o = torch.matmul(p, kv[..., nope:].contiguous())                      # [b, h, n, v]
+    # K^T and V with the key dimension padded to a multiple of 8 (zeros), so the
+    # score rows are 16-byte aligned for any L and the padding adds exact zeros
+    Lp = (L + 7) // 8 * 8
+    kT = torch.zeros((b, h, nope + r, Lp), dtype=torch.bfloat16, device=q.device)
+    kT[..., :nope, :L].copy_(kv[..., :nope].transpose(-1, -2))
+    kT[..., nope:, :L].copy_(k_rot.transpose(-1, -2).expand(b, h, r, L))
+    vp = torch.zeros((b, h, Lp, vd), dtype=torch.bfloat16, device=q.device)
+    vp[:, :, :L].copy_(kv[..., nope:])
+    scores = torch.matmul(qf, kT)                                          # bf16 [b, h, n, Lp]
+    p = ops.attn_softmax_(scores, W.softmax_scale, causal=True, kv_len=L)
+    o = torch.matmul(p, vp)                                                # [b, h, n, v]
     return o.transpose(1, 2).reshape(b, n, h * vd)
 
 
@@ -277,7 +284,7 @@ def _decode_step(x: torch.Tensor, W: MLAWeights, cache: LatentKVCache, rows: tor
         else:
             rows.copy_(ops.linear(x2, W.kva).view(b, n, lora + r))
     L = cache.current_len
-    if n >= UP_PROJECTED_MIN_TOKENS and L % 8 == 0 and L <= 4096:
+    if n >= UP_PROJECTED_MIN_TOKENS:
         o = _attend_up_projected(q.view(b, n, h, nope + r), cache, W, cos, sin, eps)
         return ops.linear(o, W.o)
     latent, k_pe = cache.get(L)

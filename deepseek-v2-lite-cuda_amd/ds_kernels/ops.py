@@ -544,37 +544,73 @@ def _rope_strides(t: torch.Tensor, name: str):
     return sb, (sh if h > 1 else 0), ss
 
 
-def attn_softmax_(scores: torch.Tensor, scale: float, causal: bool = True) -> torch.Tensor:
-    """In place over bf16 scores [..., q_len, kv_len] (last dim contiguous, rows
-    16-byte aligned): softmax_fp32(bf16(scores * scale) + causal mask) rounded to
-    bf16, the eager sequence of DeepSeekMLA.forward (mla.py:366-381) in one pass.
-    Query i sees keys j <= i + kv_len - q_len when causal. Returns scores."""
+def attn_softmax_(scores: torch.Tensor, scale: float, causal: bool = True,
+                  kv_len: int = None, mask: torch.Tensor = None) -> torch.Tensor:
+    """In place over bf16 scores [..., q_len, L] (last dim contiguous, rows
+    16-byte aligned): softmax_fp32(bf16(scores * scale) + mask) rounded to bf16,
+    the eager sequence of DeepSeekMLA.forward (mla.py:366-381) in one pass.
+    kv_len: the number of keys (default L); the columns kv_len.. up to the next
+    multiple of 8 are written as 0, so a score buffer padded to 16-byte rows
+    feeds P.V with exact zeros. causal: query i sees keys j <= i + kv_len - q_len.
+    mask: an additive attention_mask (bf16 or fp32, -inf where masked)
+    broadcastable to [b, h, q_len, kv_len] for 4-D scores [b, h, q_len, L]
+    (mla.py:374: `attn_weights + attention_mask`, in the dtype torch promotes
+    the sum to), applied in place of the causal mask when causal is False.
+    Returns scores."""
     op = "attn_softmax"
     _req(scores.is_cuda, f"{op}: scores must be a CUDA tensor.")
     _dtype(scores, torch.bfloat16, "scores", op)
     _req(scores.dim() >= 2 and scores.stride(-1) == 1, f"{op}: last dim must be contiguous.")
-    q_len, kv_len = scores.shape[-2], scores.shape[-1]
-    flat = scores.view(-1, kv_len) if scores.is_contiguous() else None
+    q_len, L = scores.shape[-2], scores.shape[-1]
+    kv_len = L if kv_len is None else int(kv_len)
+    _req(0 < kv_len <= L and (kv_len + 7) // 8 * 8 <= L,
+         f"{op}: kv_len {kv_len} must be in 1..{L} with room for its 8-key padding.")
+    flat = scores.view(-1, L) if scores.is_contiguous() else None
     _req(flat is not None, f"{op}: scores must be contiguous.")
     rows = flat.shape[0]
-    if rows:
+    if not rows:
+        return scores
+    st = stream_handle(scores.device)
+    if mask is None:
         with torch.cuda.device(scores.device):
-            check(lib.dsk_attn_softmax(flat.data_ptr(), kv_len, rows, kv_len, q_len,
-                                       float(scale), 1 if causal else 0,
-                                       stream_handle(scores.device)), op)
+            check(lib.dsk_attn_softmax(flat.data_ptr(), L, rows, kv_len, q_len, float(scale),
+                                       1 if causal else 0, st), op)
+        return scores
+    _req(scores.dim() == 4, f"{op}: a mask needs 4-D scores [b, h, q_len, L].")
+    _req(mask.is_cuda and mask.device == scores.device, f"{op}: mask must be on the scores' device.")
+    _req(mask.dtype in (torch.bfloat16, torch.float32), f"{op}: mask must be bf16 or fp32.")
+    b, h = scores.shape[0], scores.shape[1]
+    _req(mask.dim() <= 4, f"{op}: mask must have at most 4 dims.")
+    m = mask.reshape((1,) * (4 - mask.dim()) + tuple(mask.shape))
+    try:
+        m = m.expand(b, h, q_len, kv_len)
+    except RuntimeError:
+        raise RuntimeError(f"{op}: mask {tuple(mask.shape)} does not broadcast to "
+                           f"[{b}, {h}, {q_len}, {kv_len}].") from None
+    if m.stride(-1) != 1:
+        m = m.contiguous()
+    with torch.cuda.device(scores.device):
+        check(lib.dsk_attn_softmax_masked(
+            flat.data_ptr(), L, rows, kv_len, q_len, h, float(scale), 1 if causal else 0,
+            m.data_ptr(), 1 if m.dtype == torch.float32 else 0, m.stride(0), m.stride(1),
+            m.stride(2), st), op)
     return scores
 
 
 def mla_attn_pack(q: torch.Tensor, kv: torch.Tensor, k_pe: torch.Tensor, cos: torch.Tensor,
-                  sin: torch.Tensor, heads: int = 16):
+                  sin: torch.Tensor, heads: int = 16, pad: bool = False):
     """The head-major operands of DeepSeekMLA.forward's attention (mla.py:354-366)
     in one pass: Q = (q_nope | rope(q_pe)) [b, h, s, 192], K^T = (k_nope |
     rope(k_pe) for every head)^T [b, h, 192, s] and V [b, h, s, 128], all
     contiguous. q: bf16 [b, s, h*192] (q_proj output, each head nope then rope
     part), kv: bf16 [b, s, h*256] (kv_b_proj output, each head k_nope then v),
     k_pe: bf16 [b, s, 64] (raw shared RoPE key); each may be a view with strided
-    rows and a contiguous last dim. cos/sin: [>= s, 64] tables by position
-    (cast to bf16, as the RoPE op uses them). s must be a multiple of 8."""
+    rows and a contiguous last dim. cos/sin: [>= s, 64] tables by position, or
+    [b, >= s, 64] per batch entry (the tables indexed by position_ids), cast to
+    bf16 as the RoPE op uses them.
+    pad: K^T and V get sp = s rounded up to 8 positions ([b, h, 192, sp],
+    [b, h, sp, 128]) with zero padding, so that s need not be a multiple of 8;
+    without it s must be."""
     op = "mla_attn_pack"
     for t, nm in ((q, "q"), (kv, "kv"), (k_pe, "k_pe"), (cos, "cos"), (sin, "sin")):
         _req(isinstance(t, torch.Tensor) and t.is_cuda, f"{op}: {nm} must be a CUDA tensor.")
@@ -587,19 +623,24 @@ def mla_attn_pack(q: torch.Tensor, kv: torch.Tensor, k_pe: torch.Tensor, cos: to
     for t, nm in ((q, "q"), (kv, "kv"), (k_pe, "k_pe")):
         _req(b <= 1 or t.stride(0) == s * t.stride(1),
              f"{op}: {nm} rows must be evenly spaced over batch and sequence.")
+    _req(pad or s % 8 == 0, f"{op}: s must be a multiple of 8 (or pass pad=True).")
     cb = cos.to(torch.bfloat16).contiguous()
     sb = sin.to(torch.bfloat16).contiguous()
-    _req(cb.dim() == 2 and cb.shape[0] >= s and cb.shape[1] == 64 and sb.shape == cb.shape,
-         f"{op}: cos/sin must be [>= s, 64].")
+    _req(sb.shape == cb.shape and cb.dim() in (2, 3) and cb.shape[-2] >= s and cb.shape[-1] == 64
+         and (cb.dim() == 2 or cb.shape[0] == b),
+         f"{op}: cos/sin must be [>= s, 64] or [b, >= s, 64].")
+    sp = (s + 7) // 8 * 8 if pad else s
     dev = q.device
     q_out = torch.empty((b, heads, s, 192), dtype=torch.bfloat16, device=dev)
-    k_t = torch.empty((b, heads, 192, s), dtype=torch.bfloat16, device=dev)
-    v = torch.empty((b, heads, s, 128), dtype=torch.bfloat16, device=dev)
+    k_t = torch.empty((b, heads, 192, sp), dtype=torch.bfloat16, device=dev)
+    v = torch.empty((b, heads, sp, 128), dtype=torch.bfloat16, device=dev)
     with torch.cuda.device(dev):
-        check(lib.dsk_mla_attn_pack(q.data_ptr(), q.stride(1), kv.data_ptr(), kv.stride(1),
-                                    k_pe.data_ptr(), k_pe.stride(1), cb.data_ptr(), sb.data_ptr(),
-                                    cb.stride(0), q_out.data_ptr(), k_t.data_ptr(), v.data_ptr(),
-                                    b, s, heads, 128, 64, 128, stream_handle(dev)), op)
+        check(lib.dsk_mla_attn_pack_ex(q.data_ptr(), q.stride(1), kv.data_ptr(), kv.stride(1),
+                                       k_pe.data_ptr(), k_pe.stride(1), cb.data_ptr(),
+                                       sb.data_ptr(), cb.stride(-2),
+                                       cb.stride(0) if cb.dim() == 3 else 0, q_out.data_ptr(),
+                                       k_t.data_ptr(), v.data_ptr(), b, s, sp, heads, 128, 64,
+                                       128, stream_handle(dev)), op)
     return q_out, k_t, v
 
 

@@ -43,6 +43,10 @@ enum {
 #define DSK_LAYOUT_ROW_MAJOR 0
 #define DSK_LAYOUT_TILED 1
 
+/* Element types of optional operands (the attention mask). */
+#define DSK_DTYPE_BF16 0
+#define DSK_DTYPE_F32 1
+
 /* Limits mirrored from the reference routing kernel (routing.cu:32-33). */
 #define DSK_MAX_EXPERTS 64
 #define DSK_MAX_TOP_K 6
@@ -302,11 +306,29 @@ int dsk_linear_batched(const dsk_bf16* x, int64_t ld_x, int64_t x_batch_stride,
  *   p = bf16(softmax_fp32(bf16(score * scale) + causal_mask)),
  * with key j of query i masked when causal and j > i + kv_len - q_len (the row's
  * query index is row % q_len). Masked probabilities are written as 0 and their
- * scores are not read. The reference has no kernel for this: it replaces four
- * torch passes over the scores (scale, mask, fp32 softmax, cast) of the
- * decoder layer's attention core. kv_len % 8 == 0, kv_len <= 4096. */
+ * scores are not read. Any kv_len >= 1: rows of up to 4096 keys are held in
+ * registers, longer ones take two passes. ld % 8 == 0 and ld >= kv_len rounded
+ * up to 8; keys kv_len.. up to that multiple of 8 are written as 0 (a 16-byte
+ * padded score buffer then multiplies zero-padded V rows exactly). A fully
+ * masked row gives NaN, as torch's softmax does. The reference has no kernel for
+ * this: it replaces four torch passes over the scores (scale, mask, fp32
+ * softmax, cast) of the decoder layer's attention core. */
 int dsk_attn_softmax(dsk_bf16* scores, int64_t ld, int64_t rows, int kv_len,
                      int q_len, float scale, int causal, void* stream);
+
+/* dsk_attn_softmax with the additive attention_mask of DeepSeekMLA.forward
+ * (mla.py:295-315,374: `attn_weights + attention_mask`, [bsz, 1, q_len, kv_len],
+ * -inf where masked) in place of (or besides) the causal mask. Rows are
+ * (batch, head, query) with the query fastest and `heads` heads per batch
+ * entry; the mask element of key j is at
+ *   mask[b * mask_sb + h * mask_sh + i * mask_sq + j]   (element strides),
+ * so a head stride of 0 broadcasts one mask over the heads. mask_dtype
+ * DSK_DTYPE_BF16 adds in bf16 (the sum rounded, as a bf16 + bf16 tensor add),
+ * DSK_DTYPE_F32 in fp32 (as torch promotes bf16 + fp32). */
+int dsk_attn_softmax_masked(dsk_bf16* scores, int64_t ld, int64_t rows, int kv_len,
+                            int q_len, int heads, float scale, int causal,
+                            const void* mask, int mask_dtype, int64_t mask_sb,
+                            int64_t mask_sh, int64_t mask_sq, void* stream);
 
 /* --------------------------------------------------- attention operand pack --
  * Packs the operands of the full-sequence attention of DeepSeekMLA.forward
@@ -328,6 +350,22 @@ int dsk_mla_attn_pack(const dsk_bf16* q, int64_t ld_q, const dsk_bf16* kv,
                       const dsk_bf16* cos_t, const dsk_bf16* sin_t, int64_t ld_cs,
                       dsk_bf16* q_out, dsk_bf16* k_t, dsk_bf16* v_out, int batch,
                       int seq, int heads, int nope, int rope, int v_dim, void* stream);
+
+/* dsk_mla_attn_pack for position_ids and any sequence length (mla.py:295-352:
+ * apply_rotary_pos_emb indexes the tables by position_ids [bsz, seq]): the
+ * tables of batch entry b start at cos_t + b * cs_batch_stride (0: one table
+ * for every entry, row s for position s), and K^T rows and V are padded to
+ * seq_pad positions (seq <= seq_pad, seq_pad % 8 == 0, seq_pad - seq < 8):
+ *   k_t [b, h, 192, seq_pad], v_out [b, h, seq_pad, 128], q_out [b, h, seq, 192],
+ * the padding columns of K^T and rows of V written as 0. With seq % 8 != 0 the
+ * products Q.K^T and P.V then run on 16-byte aligned rows and the padding
+ * adds exact zeros. */
+int dsk_mla_attn_pack_ex(const dsk_bf16* q, int64_t ld_q, const dsk_bf16* kv,
+                         int64_t ld_kv, const dsk_bf16* k_pe, int64_t ld_kpe,
+                         const dsk_bf16* cos_t, const dsk_bf16* sin_t, int64_t ld_cs,
+                         int64_t cs_batch_stride, dsk_bf16* q_out, dsk_bf16* k_t,
+                         dsk_bf16* v_out, int batch, int seq, int seq_pad, int heads,
+                         int nope, int rope, int v_dim, void* stream);
 
 /* ----------------------------------------------- latent-cache decode attention --
  * Absorbed multi-head latent attention of new tokens over the latent KV cache

@@ -6,7 +6,8 @@ References (sahan974/DeepSeek-V2-Lite-CUDA):
   src/reference/mla.py:70-96    YaRN helpers (correction dim/range, mscale, ramp mask)
   src/reference/mla.py:108-165  YaRN tables: inv_freq blend, emb = cat(freqs, freqs), cos/sin * mscale
   src/reference/mla.py:176-206  rotate_half + deinterleave + (x*cos) + (rotate_half(x)*sin)
-  src/reference/mla.py:295-393  DeepSeekMLA.forward (eager attention, causal)
+  src/reference/mla.py:295-393  DeepSeekMLA.forward (eager attention; causal or an additive
+                                attention_mask; position_ids index the RoPE tables)
   src/reference/decoder_layer.py:108-139  pre-norm -> MLA -> residual -> pre-norm -> MoE -> residual
 """
 from __future__ import annotations
@@ -121,40 +122,67 @@ def mla_projections(x, w_q, w_kva, w_kva_norm, w_kvb, cos, sin, n_heads=16, nope
     return q_nope, rope(q_pe, c, sn), k_nope, v, rope(k_pe, c, sn), ln
 
 
-def attention(q, k, v, scale):
-    """mla.py:356-384: softmax(q k^T * scale + causal mask) v, fp32."""
-    s = q.shape[-2]
-    scores = (q @ np.swapaxes(k, -1, -2)) * f32(scale)
-    mask = np.triu(np.ones((s, s), bool), k=1)
-    scores = np.where(mask, -np.inf, scores)
-    scores = scores - scores.max(axis=-1, keepdims=True)
-    p = np.exp(scores)
-    p = p / p.sum(axis=-1, keepdims=True)
-    return (p @ v).astype(f32)
+def attention(q, k, v, scale, mask=None):
+    """mla.py:356-384: softmax(q k^T * scale + mask) v in fp32, per (batch, head)
+    to bound memory. mask None: the causal mask (mla.py:368-373); otherwise the
+    additive attention_mask broadcast to [b, h, s, s] (mla.py:374-375)."""
+    b, h, s = q.shape[0], q.shape[1], q.shape[-2]
+    causal = np.triu(np.ones((s, s), bool), k=1) if mask is None else None
+    mk = None if mask is None else np.broadcast_to(np.asarray(mask, f32), (b, h, s, k.shape[-2]))
+    out = np.empty(q.shape[:-1] + (v.shape[-1],), f32)
+    for bi in range(b):
+        for hi in range(h):
+            kk = k[bi, hi if k.shape[1] > 1 else 0]
+            sc = (q[bi, hi] @ kk.T).astype(f32) * f32(scale)
+            sc = np.where(causal, -np.inf, sc) if mk is None else sc + mk[bi, hi]
+            sc = sc - sc.max(axis=-1, keepdims=True)
+            p = np.exp(sc)
+            p = p / p.sum(axis=-1, keepdims=True)
+            out[bi, hi] = p @ v[bi, hi if v.shape[1] > 1 else 0]
+    return out
+
+
+def tables_at(cos, sin, position_ids):
+    """mla.py:186-187: cos[position_ids], sin[position_ids] -> [b, 1, s, d] (or the
+    [1, 1, s, d] tables for positions 0..s-1 when position_ids is None)."""
+    if position_ids is None:
+        return cos[None, None], sin[None, None]
+    pid = np.asarray(position_ids)
+    return cos[pid][:, None], sin[pid][:, None]
 
 
 def mla_forward(x, w_q, w_kva, w_kva_norm, w_kvb, w_o, n_heads=16, nope=128, rope_dim=64,
-                v_dim=128, kv_lora=512, eps=1e-6, factor=40.0):
-    """DeepSeekMLA.forward (mla.py:295-393), fp32, positions 0..s-1, causal."""
+                v_dim=128, kv_lora=512, eps=1e-6, factor=40.0, attention_mask=None,
+                position_ids=None):
+    """DeepSeekMLA.forward (mla.py:295-393), fp32. position_ids [b, s] index the
+    tables of the first s positions (default 0..s-1, mla.py:310-312);
+    attention_mask: additive [b, 1, s, s] replacing the causal mask."""
     b, s, _ = x.shape
     cos, sin = yarn_cos_sin(s, rope_dim, factor=factor)
-    q_nope, q_rot, k_nope, v, k_rot, _ = mla_projections(
-        x, w_q, w_kva, w_kva_norm, w_kvb, cos, sin, n_heads, nope, rope_dim, v_dim, kv_lora, eps)
-    q = np.concatenate([q_nope, q_rot], axis=-1)
-    k = np.concatenate([k_nope, np.broadcast_to(k_rot, k_nope.shape[:-1] + (rope_dim,))], axis=-1)
+    c, sn = tables_at(cos, sin, position_ids)
+    q = linear(x, w_q).reshape(b, s, n_heads, nope + rope_dim).transpose(0, 2, 1, 3)
+    kv_a = linear(x, w_kva)
+    k_pe = kv_a[..., kv_lora:].reshape(b, s, 1, rope_dim).transpose(0, 2, 1, 3)
+    ln = rms_norm(kv_a[..., :kv_lora], w_kva_norm, eps)
+    kv = linear(ln, w_kvb).reshape(b, s, n_heads, nope + v_dim).transpose(0, 2, 1, 3)
+    q_rot, k_rot = rope(q[..., nope:], c, sn), rope(k_pe, c, sn)
+    qf = np.concatenate([q[..., :nope], q_rot], axis=-1)
+    k = np.concatenate([kv[..., :nope], np.broadcast_to(k_rot, (b, n_heads, s, rope_dim))],
+                       axis=-1)
     m = yarn_get_mscale(factor, 0.707)
     scale = (nope + rope_dim) ** -0.5 * m * m                      # mla.py:287-288
-    o = attention(q, k, v, scale)
+    o = attention(qf, k, kv[..., nope:], scale, attention_mask)
     o = o.transpose(0, 2, 1, 3).reshape(b, s, n_heads * v_dim)
     return linear(o, w_o)
 
 
-def decoder_layer(x, p: dict, top_k=6, eps=1e-6):
+def decoder_layer(x, p: dict, top_k=6, eps=1e-6, attention_mask=None, position_ids=None):
     """DeepSeekDecoderLayer.forward (decoder_layer.py:108-139), fp32.
     p: dict with in_norm, q, kva, kva_norm, kvb, o, post_norm, wg, gates, ups,
     downs, shared (tuple or None)."""
     h = rms_norm(x, p["in_norm"], eps)
-    h = mla_forward(h, p["q"], p["kva"], p["kva_norm"], p["kvb"], p["o"], eps=eps)
+    h = mla_forward(h, p["q"], p["kva"], p["kva_norm"], p["kvb"], p["o"], eps=eps,
+                    attention_mask=attention_mask, position_ids=position_ids)
     x = x + h
     h = rms_norm(x, p["post_norm"], eps)
     b, s, H = h.shape

@@ -36,7 +36,7 @@ def test_every_declared_symbol_is_exported(dsk):
 
 
 def test_abi_version(dsk):
-    assert dsk.lib.dsk_abi_version() == 2
+    assert dsk.lib.dsk_abi_version() == 3
 
 
 def _err(dsk):
@@ -130,14 +130,33 @@ def test_linear_ex_validation(dsk):
 
 def test_attn_softmax_validation(dsk):
     lib = dsk.lib
+    # rows padded to 8 keys: ld must cover kv_len rounded up to 8 and be a multiple of 8
     rc = lib.dsk_attn_softmax(16, 100, 64, 100, 8, 0.1, 1, None)
-    assert rc == 1 and "multiple of 8" in _err(dsk)
-    rc = lib.dsk_attn_softmax(16, 8192, 64, 8192, 8, 0.1, 1, None)
-    assert rc == 1 and "4096" in _err(dsk)
+    assert rc == 3 and "rounded up to 8" in _err(dsk)
+    rc = lib.dsk_attn_softmax(16, 104, 64, 105, 8, 0.1, 1, None)
+    assert rc == 3 and "rounded up to 8" in _err(dsk)
+    rc = lib.dsk_attn_softmax(None, 104, 64, 100, 8, 0.1, 1, None)
+    assert rc == 2       # a valid padded shape gets past the size checks
+    rc = lib.dsk_attn_softmax(None, 8192, 64, 8192, 8, 0.1, 1, None)
+    assert rc == 2       # rows longer than 4096 keys are accepted (two-pass kernel)
     rc = lib.dsk_attn_softmax(16, 64, 60, 64, 8, 0.1, 1, None)
     assert rc == 1 and "q_len" in _err(dsk)
     rc = lib.dsk_attn_softmax(16, 64, 64, 64, 128, 0.1, 1, None)
     assert rc == 1 and "q_len" in _err(dsk)
+
+
+def test_attn_softmax_masked_validation(dsk):
+    lib = dsk.lib
+    # mask dtype must be bf16 (0) or fp32 (1)
+    rc = lib.dsk_attn_softmax_masked(16, 64, 64, 64, 8, 1, 0.1, 0, 16, 7, 0, 0, 64, None)
+    assert rc == 1 and "mask dtype" in _err(dsk)
+    # rows / q_len must be a multiple of heads
+    rc = lib.dsk_attn_softmax_masked(16, 64, 64, 64, 8, 3, 0.1, 0, 16, 1, 0, 0, 64, None)
+    assert rc == 1 and "heads" in _err(dsk)
+    rc = lib.dsk_attn_softmax_masked(16, 64, 64, 64, 8, 2, 0.1, 0, None, 1, 0, 0, 64, None)
+    assert rc == 2 and "mask" in _err(dsk)
+    assert lib.dsk_attn_softmax_masked(None, 64, 0, 64, 8, 2, 0.1, 0, None, 1, 0, 0, 64,
+                                       None) == 0
 
 
 def test_linear_rows_validation(dsk):
@@ -172,6 +191,19 @@ def test_attn_pack_validation(dsk):
     assert call(out=24) == 3 and call(ld_kpe=3650) == 3
     assert call(ld_q=3064) == 1 and "row stride" in _err(dsk)
     assert call(ld_kv=4088) == 1 and call(ld_cs=56) == 1
+
+
+def test_attn_pack_ex_validation(dsk):
+    lib = dsk.lib
+
+    def call(seq=60, seq_pad=64, cs_bs=0, q=16):
+        return lib.dsk_mla_attn_pack_ex(q, 3648, 16, 4096, 16, 3648, 16, 16, 64, cs_bs, 16, 16,
+                                        16, 2, seq, seq_pad, 16, 128, 64, 128, None)
+    assert call(q=None) == 2                    # seq 60 padded to 64 passes the size checks
+    assert call(seq_pad=60) == 1 and "seq_pad" in _err(dsk)
+    assert call(seq_pad=72) == 1 and "seq_pad" in _err(dsk)
+    assert call(cs_bs=4) == 3                   # per-batch tables must start 16-byte aligned
+    assert call(cs_bs=-64) == 1 and "stride" in _err(dsk)
 
 
 def test_mla_decode_validation(dsk):
@@ -301,7 +333,7 @@ def test_c_caller_links_and_calls(dsk, tmp_path):
 #include <string.h>
 #include "dsk.h"
 int main(void) {
-  if (dsk_abi_version() != 2) return 1;
+  if (dsk_abi_version() != 3) return 1;
   /* top_k = 7 is rejected before any device work */
   int rc = dsk_moe_routing(NULL, 64, NULL, NULL, NULL, 4, 64, 7, NULL, 0, NULL);
   if (rc != 1 || strstr(dsk_last_error(), "top_k") == NULL) return 2;

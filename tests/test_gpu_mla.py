@@ -241,12 +241,16 @@ def test_mla_projections_fused_norm_matches_separate_pass(mla_setup):
         assert max_rel_err(np32(fused[i]), np32(sep[i])) <= BF16_TOL
 
 
-def _softmax_ref(sc: torch.Tensor, scale: float, causal: bool) -> torch.Tensor:
+def _softmax_ref(sc: torch.Tensor, scale: float, causal: bool, mask=None) -> torch.Tensor:
     """CPU fp32 restatement of mla.py:366-381 on the same bf16 scores: scores *
     scale rounded to bf16, causal mask (query i of the last q_len positions sees
-    keys j <= i + kv_len - q_len), softmax in fp32 (torch), rounded to bf16."""
+    keys j <= i + kv_len - q_len) or the additive mask added in the dtype torch
+    promotes bf16 + mask to, softmax in fp32 (torch), rounded to bf16."""
     q_len, kv_len = sc.shape[-2:]
-    x = (sc.float() * scale).to(torch.bfloat16).float()
+    x = (sc.float() * scale).to(torch.bfloat16)
+    if mask is not None:
+        x = x + mask                    # bf16 + bf16 -> bf16, bf16 + fp32 -> fp32
+    x = x.float()
     if causal:
         i = torch.arange(q_len)[:, None]
         j = torch.arange(kv_len)[None, :]
@@ -256,7 +260,9 @@ def _softmax_ref(sc: torch.Tensor, scale: float, causal: bool) -> torch.Tensor:
 
 @pytest.mark.parametrize("shape,causal", [((2, 3, 64, 64), True), ((1, 2, 40, 520), True),
                                           ((2, 16, 128, 2048), True), ((1, 1, 8, 4096), True),
-                                          ((3, 5, 16, 1024), False), ((4, 7, 72), False)])
+                                          ((3, 5, 16, 1024), False), ((4, 7, 72), False),
+                                          ((1, 2, 24, 4104), True), ((2, 1, 5, 6000), False),
+                                          ((1, 1, 3, 9000), True)])
 def test_attn_softmax_matches_torch(dsk, shape, causal):
     g = torch.Generator().manual_seed(sum(shape))
     sc = (torch.randn(*shape, generator=g) * 6).to(torch.bfloat16)
@@ -273,6 +279,49 @@ def test_attn_softmax_matches_torch(dsk, shape, causal):
         j = torch.arange(kv_len)[None, :]
         assert bool((out.float()[..., j > i + (kv_len - q_len)] == 0).all())
     np.testing.assert_allclose(out.float().sum(-1).numpy(), 1.0, atol=2e-2)
+
+
+@pytest.mark.parametrize("kv_len,causal", [(100, True), (1, False), (4099, True), (13, False)])
+def test_attn_softmax_padded_rows(dsk, kv_len, causal):
+    """kv_len keys in rows padded to a multiple of 8: the probabilities of the
+    first kv_len columns as the unpadded reference, the padding columns exactly 0
+    (a P.V product over zero-padded V rows then adds nothing)."""
+    L = (kv_len + 7) // 8 * 8
+    q_len = min(kv_len, 24) if causal else 7
+    g = torch.Generator().manual_seed(kv_len)
+    sc = (torch.randn(2, 3, q_len, L, generator=g) * 4).to(torch.bfloat16)
+    ref = _softmax_ref(sc[..., :kv_len], 0.13, causal)
+    out = dsk.attn_softmax_(sc.to(DEV), 0.13, causal=causal, kv_len=kv_len).cpu()
+    assert float((out[..., :kv_len].float() - ref.float()).abs().max()) <= \
+        2 ** -7 * float(ref.float().abs().max())
+    assert bool((out[..., kv_len:] == 0).all())
+
+
+@pytest.mark.parametrize("mdtype,shape", [(torch.bfloat16, (2, 3, 40, 40)),
+                                          (torch.float32, (2, 3, 40, 40)),
+                                          (torch.float32, (1, 4, 17, 4100)),
+                                          (torch.bfloat16, (2, 2, 33, 33))])
+def test_attn_softmax_additive_mask(dsk, mdtype, shape):
+    """The additive attention_mask of mla.py:374 ([b, 1, q, kv], broadcast over
+    the heads): a causal-plus-padding mask with -inf entries and finite biases,
+    added in the promoted dtype, against torch's fp32 softmax of the same sum."""
+    b, h, q_len, kv_len = shape
+    g = torch.Generator().manual_seed(q_len * 7 + kv_len)
+    L = (kv_len + 7) // 8 * 8
+    sc = (torch.randn(b, h, q_len, L, generator=g) * 5).to(torch.bfloat16)
+    i = torch.arange(q_len)[:, None] + (kv_len - q_len)
+    j = torch.arange(kv_len)[None, :]
+    m = torch.randn(b, 1, q_len, kv_len, generator=g) * 2        # finite biases
+    m = m.masked_fill(j > i, float("-inf"))                      # causal
+    m[-1, :, :, kv_len - kv_len // 4:] = float("-inf")           # last sequence padded
+    m[-1, :, :, 0] = 0.0                                         # no row fully masked
+    m = m.to(mdtype)
+    ref = _softmax_ref(sc[..., :kv_len], 0.2, False, mask=m)
+    out = dsk.attn_softmax_(sc.to(DEV), 0.2, causal=False, kv_len=kv_len, mask=m.to(DEV)).cpu()
+    assert float((out[..., :kv_len].float() - ref.float()).abs().max()) <= \
+        2 ** -7 * float(ref.float().abs().max())
+    assert bool((out[..., :kv_len][ref == 0] == 0).all())
+    assert bool((out[..., kv_len:] == 0).all())
 
 
 # ------------------------------------------- configs 3 and 4 (composition) --
@@ -432,3 +481,105 @@ def test_config4_decoder_layer_full_size_properties(mla_setup):
     one = dm.decoder_layer_forward(x[2:3].contiguous(), P, cos, sin)
     torch.cuda.synchronize()
     assert max_rel_err(np32(one), np32(out1[2:3])) <= BF16_TOL
+
+
+def _decoder_params(M, wn):
+    return {"in_norm": np.ones(2048, np.float32), "post_norm": np.ones(2048, np.float32),
+            "q": wn["q"], "kva": wn["kva"], "kva_norm": wn["kva_norm"], "kvb": wn["kvb"],
+            "o": wn["o"], "wg": _bf(M.wg), "gates": _bf(M.gates), "ups": _bf(M.ups),
+            "downs": _bf(M.downs), "shared": tuple(_bf(t) for t in M.shared)}
+
+
+@pytest.mark.parametrize("b,s", [(2, 100), (1, 13), (1, 1)])
+def test_mla_forward_any_length(mla_setup, b, s):
+    """DeepSeekMLA.forward at sequence lengths that are not multiples of 8
+    (K^T, scores and V padded to 16-byte rows with zeros) against the oracle."""
+    dm, w, W, wn = mla_setup
+    g = torch.Generator().manual_seed(100 + s)
+    x = torch.randn(b, s, 2048, generator=g).to(torch.bfloat16)
+    cos, sin = dm.yarn_cos_sin(s)
+    out = dm.mla_forward(x.to(DEV), W, cos.to(DEV), sin.to(DEV))
+    ref = ol.mla_forward(np32(x), wn["q"], wn["kva"], wn["kva_norm"], wn["kvb"], wn["o"])
+    assert out.shape == (b, s, 2048)
+    assert max_rel_err(np32(out), ref) <= BF16_TOL
+
+
+def _padding_mask(b, s, pad, dtype):
+    """Additive [b, 1, s, s]: causal, and the last `pad` positions of sequence
+    b-1 are padding no query attends to (mla.py:295-315 attention_mask)."""
+    i = torch.arange(s)[:, None]
+    j = torch.arange(s)[None, :]
+    m = torch.zeros(b, 1, s, s).masked_fill(j > i, float("-inf"))
+    m[b - 1, :, :, s - pad:] = float("-inf")
+    m[b - 1, :, s - pad:, 0] = 0.0          # padded queries still see key 0
+    return m.to(dtype)
+
+
+@pytest.mark.parametrize("mdtype", [torch.bfloat16, torch.float32])
+def test_mla_forward_padded_batch_mask_and_positions(mla_setup, mdtype):
+    """A padded batch as a serving stack builds it: an additive mask that hides
+    the second sequence's padding, and per-sequence position_ids (the padded
+    sequence's positions restart after a left shift), against the oracle's
+    forward with the same mask and positions (mla.py:295-315, 349-352, 374)."""
+    dm, w, W, wn = mla_setup
+    b, s, pad = 2, 64, 16
+    g = torch.Generator().manual_seed(71)
+    x = torch.randn(b, s, 2048, generator=g).to(torch.bfloat16)
+    m = _padding_mask(b, s, pad, mdtype)
+    pid = torch.stack([torch.arange(s), torch.cat([torch.arange(s - pad),
+                                                   torch.zeros(pad, dtype=torch.long)])])
+    cos, sin = dm.yarn_cos_sin(s)
+    out = dm.mla_forward(x.to(DEV), W, cos.to(DEV), sin.to(DEV), attention_mask=m.to(DEV),
+                         position_ids=pid.to(DEV))
+    ref = ol.mla_forward(np32(x), wn["q"], wn["kva"], wn["kva_norm"], wn["kvb"], wn["o"],
+                         attention_mask=m.float().numpy(), position_ids=pid.numpy())
+    assert max_rel_err(np32(out), ref) <= BF16_TOL
+    # the unpadded rows of sequence 1 do not depend on what sits in its padding
+    x2 = x.clone()
+    x2[1, s - pad:] = torch.randn(pad, 2048, generator=g).to(torch.bfloat16)
+    out2 = dm.mla_forward(x2.to(DEV), W, cos.to(DEV), sin.to(DEV), attention_mask=m.to(DEV),
+                          position_ids=pid.to(DEV))
+    assert max_rel_err(np32(out2[1, :s - pad]), np32(out[1, :s - pad])) <= BF16_TOL / 4
+
+
+def test_mla_forward_position_ids_out_of_range(mla_setup):
+    dm, w, W, wn = mla_setup
+    x = torch.zeros(1, 8, 2048, dtype=torch.bfloat16, device=DEV)
+    cos, sin = dm.yarn_cos_sin(8, device=DEV)
+    with pytest.raises(IndexError):
+        dm.mla_forward(x, W, cos, sin, position_ids=torch.full((1, 8), 8, device=DEV))
+
+
+def test_decoder_layer_mask_and_positions(mla_setup):
+    """Config 4's layer with an attention_mask and position_ids (b=2, s=40)
+    against the oracle decoder layer (decoder_layer.py:108-130)."""
+    dm, w, W, wn = mla_setup
+    from ds_kernels import synthetic as syn
+    M = syn.moe_weights()
+    P = dm.DecoderLayerWeights.from_tensors(w, M, torch.device(DEV))
+    b, s, pad = 2, 40, 8
+    g = torch.Generator().manual_seed(72)
+    x = torch.randn(b, s, 2048, generator=g).to(torch.bfloat16)
+    m = _padding_mask(b, s, pad, torch.bfloat16)
+    pid = torch.stack([torch.arange(s), torch.arange(s).flip(0)])
+    cos, sin = dm.yarn_cos_sin(s)
+    out = dm.decoder_layer_forward(x.to(DEV), P, cos.to(DEV), sin.to(DEV),
+                                   attention_mask=m.to(DEV), position_ids=pid.to(DEV))
+    ref = ol.decoder_layer(np32(x), _decoder_params(M, wn), attention_mask=m.float().numpy(),
+                           position_ids=pid.numpy())
+    assert max_rel_err(np32(out), ref) <= BF16_TOL
+    upd, rupd = np32(out) - np32(x), ref - np32(x)
+    assert max_rel_err(upd, rupd) <= 4 * BF16_TOL
+
+
+def test_mla_forward_longer_than_4096(mla_setup):
+    """s = 4100 > 4096 (score rows take the two-pass softmax, keys padded to
+    4104) against the oracle forward."""
+    dm, w, W, wn = mla_setup
+    b, s = 1, 4100
+    g = torch.Generator().manual_seed(73)
+    x = torch.randn(b, s, 2048, generator=g).to(torch.bfloat16)
+    cos, sin = dm.yarn_cos_sin(s)
+    out = dm.mla_forward(x.to(DEV), W, cos.to(DEV), sin.to(DEV))
+    ref = ol.mla_forward(np32(x), wn["q"], wn["kva"], wn["kva_norm"], wn["kvb"], wn["o"])
+    assert max_rel_err(np32(out), ref) <= BF16_TOL

@@ -53,7 +53,7 @@ def _run_steps(setup, x, steps):
     (1, [50, 1, 1, 1, 7, 1]),          # prefill, single steps, a multi-token step
     (2, [127, 1, 1, 1]),               # crosses the 64-key chunk boundary at 128
     (2, [63, 2, 64, 1]),
-    (1, [700, 1, 5]),                  # many blocks (700 is not a multiple of 8: absorbed kernel)
+    (1, [700, 1, 5]),                  # 700 keys, not a multiple of 8: padded prompt path
     (2, [256, 1, 130]),                # prompt through up-projected K/V, then the kernel (merge)
     (1, [1, 255, 8]),                  # up-projected step over a one-token prefix
     (3, [40, 1, 1]),                   # 3 sequences: the few-row projections at 3 rows
@@ -75,6 +75,27 @@ def test_decode_matches_full_sequence_oracle(setup, b, steps):
         e = max_rel_err(np32(out[:, pos:pos + n]), ref[:, pos:pos + n])
         assert e <= BF16_TOL, f"rows {pos}..{pos + n}: {e:.3e}"
         pos += n
+
+
+def test_decode_prompt_longer_than_4096(setup):
+    """A 4100-token prompt through the up-projected path (keys padded to 4104,
+    the two-pass softmax beyond 4096 keys), then one decode step through the
+    absorbed kernel over 4101 cached tokens, against the oracle's full-sequence
+    forward at 4101 positions."""
+    dsk, W, A, wn, _, _ = setup
+    from ds_kernels import mla as dm
+    S = 4101
+    cos, sin = dm.yarn_cos_sin(S)
+    cos, sin = cos.to(torch.bfloat16).to(DEV), sin.to(torch.bfloat16).to(DEV)
+    g = torch.Generator().manual_seed(4100)
+    x = torch.randn(1, S, 2048, generator=g).to(torch.bfloat16)
+    cache = dsk.LatentKVCache(1, S, device=DEV)
+    o1 = dsk.mla_decode_forward(x[:, :S - 1].to(DEV), W, cache, cos, sin, A)
+    o2 = dsk.mla_decode_forward(x[:, S - 1:].to(DEV), W, cache, cos, sin, A)
+    out = torch.cat([o1, o2], 1).cpu()
+    ref = _oracle(x, wn)
+    assert max_rel_err(np32(out), ref) <= BF16_TOL
+    assert max_rel_err(np32(out[:, S - 1:]), ref[:, S - 1:]) <= BF16_TOL
 
 
 def test_cache_holds_raw_projection_rows(setup):

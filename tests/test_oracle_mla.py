@@ -107,3 +107,70 @@ def test_mla_forward_causal_and_shapes():
     y2 = ol.mla_forward(x2, **p, **kw)
     np.testing.assert_allclose(y[:, :5], y2[:, :5], rtol=1e-5, atol=1e-5)
     assert not np.allclose(y[:, 5:], y2[:, 5:])
+
+
+def test_attention_additive_mask_matches_torch_sdpa():
+    """The additive-mask branch (mla.py:374-375) against SDPA's float attn_mask,
+    with a [b, 1, s, s] mask broadcast over the heads and -inf entries."""
+    rng = np.random.default_rng(6)
+    q, k, v = (rng.standard_normal((2, 3, 11, 24)).astype(np.float32) for _ in range(3))
+    m = rng.standard_normal((2, 1, 11, 11)).astype(np.float32)
+    m[0, 0, :, 7:] = -np.inf
+    m[1, 0, 3, :5] = -np.inf
+    out = ol.attention(q, k, v, 0.25, m)
+    ref = F.scaled_dot_product_attention(torch.from_numpy(q), torch.from_numpy(k),
+                                         torch.from_numpy(v), attn_mask=torch.from_numpy(m),
+                                         scale=0.25)
+    np.testing.assert_allclose(out, ref.numpy(), rtol=1e-5, atol=1e-5)
+
+
+def _small_mla():
+    rng = np.random.default_rng(8)
+    H, nh, nope, r, vd, kl = 64, 2, 16, 8, 16, 32
+    p = dict(w_q=rng.standard_normal((nh * (nope + r), H)) * 0.1,
+             w_kva=rng.standard_normal((kl + r, H)) * 0.1, w_kva_norm=np.ones(kl),
+             w_kvb=rng.standard_normal((nh * (nope + vd), kl)) * 0.1,
+             w_o=rng.standard_normal((H, nh * vd)) * 0.1)
+    p = {k: v.astype(np.float32) for k, v in p.items()}
+    return rng, H, p, dict(n_heads=nh, nope=nope, rope_dim=r, v_dim=vd, kv_lora=kl)
+
+
+def test_mla_forward_position_ids_and_mask_relabel_invariance():
+    """Tokens presented in a shuffled order with position_ids = their original
+    positions and the causal mask of those positions give the original rows,
+    shuffled: pins the position_ids table lookup (mla.py:186-187) and the
+    additive-mask path together against the default causal forward."""
+    rng, H, p, kw = _small_mla()
+    s = 12
+    x = rng.standard_normal((1, s, H)).astype(np.float32)
+    y = ol.mla_forward(x, **p, **kw)
+    perm = rng.permutation(s)
+    pid = perm[None, :]
+    m = np.where(perm[None, :] > perm[:, None], -np.inf, 0.0).astype(np.float32)[None, None]
+    y2 = ol.mla_forward(x[:, perm], **p, **kw, attention_mask=m, position_ids=pid)
+    np.testing.assert_allclose(y2, y[:, perm], rtol=1e-4, atol=1e-5)
+    # the explicit causal mask and arange positions are the defaults
+    causal = np.triu(np.full((s, s), -np.inf, np.float32), 1)[None, None]
+    y3 = ol.mla_forward(x, **p, **kw, attention_mask=causal, position_ids=np.arange(s)[None])
+    np.testing.assert_allclose(y3, y, rtol=1e-6, atol=1e-6)
+
+
+def test_mla_forward_positions_shift_invariance():
+    """RoPE makes q.k depend on the position difference only: shifting every
+    position of a sequence by the same amount (inside the table) leaves the
+    attention output unchanged up to rounding, while a non-uniform change does
+    not (mla.py:196-205 with tables indexed by position_ids)."""
+    rng, H, p, kw = _small_mla()
+    s = 16
+    x = rng.standard_normal((1, s, H)).astype(np.float32)
+    base = np.concatenate([np.arange(8), np.full(8, 7)])[None]    # 8 tokens, then padding
+    i = np.arange(s)
+    m = np.where(i[None, :] > i[:, None], -np.inf, 0.0).astype(np.float32)
+    m[:, 8:] = -np.inf
+    m = m[None, None]
+    y = ol.mla_forward(x, **p, **kw, attention_mask=m, position_ids=base)
+    y_shift = ol.mla_forward(x, **p, **kw, attention_mask=m, position_ids=base + 5)
+    np.testing.assert_allclose(y_shift[:, :8], y[:, :8], rtol=1e-4, atol=1e-5)
+    y_bad = ol.mla_forward(x, **p, **kw, attention_mask=m,
+                           position_ids=base * np.array([[1] * 4 + [2] * 12]))
+    assert not np.allclose(y_bad[:, :8], y[:, :8], rtol=1e-4, atol=1e-5)
