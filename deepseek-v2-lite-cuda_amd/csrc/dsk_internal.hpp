@@ -22,6 +22,8 @@ struct GemmArgs {
   int up_row_offset;       // SwiGLU: first up row inside a group's weight
   int max_group_rows;      // upper bound on any group's row count known to the host
                            // (0: unknown, M is used); selects the small-group kernel
+  int offsets_sorted;      // offsets never decrease (the fused layer's own): the small-
+                           // group grid then launches min(G, M) group ordinals, else G
   int64_t a_group_stride;  // skinny kernel: elements between the A bases of consecutive
   int64_t c_group_stride;  // groups, and of the C bases (0: one base, rows by offsets)
   int b_tiled;             // B stored as MFMA fragments (see the fragment-tiled layout in
@@ -69,6 +71,7 @@ constexpr int kRouteInGemmTokens = 1;
 constexpr int kRouteInGemmSlots = 256;  // routed + always-on rows the prologue maps
 
 int run_gemm(const GemmArgs& a, bool swiglu, hipStream_t st);
+
 
 // Router logits for routing = sum over n_parts partial-sum planes
 // (logits + s * part_stride, s < n_parts, fixed order) + bias[e] if given.

@@ -16,11 +16,11 @@
 // MFMAs. The partial sums meet in LDS in a fixed order (waves 1..15 into
 // wave 0), so the result is the same on every run.
 #include "dsk_internal.hpp"
+#include "gate_parts.hpp"
 
 namespace dsk {
 
 constexpr int kGateWaves = 16;
-constexpr int kGateChunk = 8;  // K steps (of 16) loaded before the MFMAs
 
 template <bool TILED>
 __global__ __launch_bounds__(64 * kGateWaves) void gate_logits_kernel(
@@ -102,46 +102,8 @@ template <bool TILED>
 __global__ __launch_bounds__(64) void gate_parts_kernel(
     const uint16_t* __restrict__ x, int64_t ld_x, const uint16_t* __restrict__ wg,
     float* __restrict__ parts, int T, int E, int H) {
-  const int lane = threadIdx.x;
-  const int t0 = blockIdx.x * 32, e0 = blockIdx.y * 32;
-  const int r32 = lane & 31, h = lane >> 5;
-  const int e = min(e0 + r32, E - 1);
-  const int t = min(t0 + r32, T - 1);
-  const int ksteps = H / 16;
-  const int s_beg = blockIdx.z * ksteps / gridDim.z;
-  const int s_end = (blockIdx.z + 1) * ksteps / gridDim.z;
-  const uint16_t* wrow = TILED ? wg + ((int64_t)blockIdx.y * ksteps) * 512 + lane * 8
-                               : wg + (int64_t)e * H + 8 * h;
-  constexpr int kWStep = TILED ? 512 : 16;
-  const uint16_t* xrow = x + (int64_t)t * ld_x + 8 * h;
-  floatx16_t acc;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) acc[r] = 0.f;
-  for (int s0 = s_beg; s0 < s_end; s0 += kGateChunk) {
-    bf16x8_t wf[kGateChunk], tf[kGateChunk];
-#pragma unroll
-    for (int u = 0; u < kGateChunk; ++u) {
-      const int s = min(s0 + u, s_end - 1);
-      wf[u] = *reinterpret_cast<const bf16x8_t*>(wrow + kWStep * s);
-      tf[u] = *reinterpret_cast<const bf16x8_t*>(xrow + 16 * s);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int u = 0; u < kGateChunk; ++u) {
-      if (s0 + u >= s_end) tf[u] = bf16x8_t{};
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[u], tf[u], acc, 0, 0, 0);
-    }
-  }
-  const int tok = t0 + r32;
-  if (tok >= T) return;
-  float* orow = parts + ((int64_t)blockIdx.z * T + tok) * E;
-#pragma unroll
-  for (int qg = 0; qg < 4; ++qg) {
-    const int eb = e0 + 8 * qg + 4 * h;
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-      if (eb + c < E) orow[eb + c] = acc[4 * qg + c];
-  }
+  gate_parts_wave<TILED>(x, ld_x, wg, parts, T, E, H, blockIdx.x, blockIdx.y, blockIdx.z,
+                         gridDim.z, threadIdx.x);
 }
 
 // K slices for the partial gate sums: more single-wave workgroups at decode

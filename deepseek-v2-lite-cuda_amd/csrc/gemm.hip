@@ -1013,9 +1013,9 @@ constexpr int skinny_batch() { return MT == 1 ? 4 : 2; }
 // after this one.
 __device__ __forceinline__ void skinny_route_prologue(const GemmArgs& p,
                                                       unsigned long long* rt_mask, int* rt_off,
-                                                      int* rt_tok, int lane, int wave) {
+                                                      int* rt_tok, int lane, int wave,
+                                                      bool store) {
   const int T = p.rt_T, E = p.rt_E, K = p.rt_K, nsh = p.rt_nsh;
-  const bool store = blockIdx.x == 0;
   if (threadIdx.x < 64) rt_mask[threadIdx.x] = 0ull;
   __syncthreads();
   const int j = lane & 15;
@@ -1071,8 +1071,10 @@ __device__ __forceinline__ void skinny_route_prologue(const GemmArgs& p,
 
 // NB: 32-row weight blocks per workgroup (SwiGLU: the gate and the up block);
 // NW: waves per workgroup, each one slice of K.
+// The kernel body, on workgroup `bid` of the small-group grid (a device function
+// so that other launches can host the same work in extra workgroups).
 template <int MT, bool SWIGLU, bool GATHER, bool TILED, int NB = 2, int NW = kSkinnyWaves>
-__global__ __launch_bounds__(64 * NW) void skinny_gemm_kernel(GemmArgs p, int n_blocks) {
+__device__ __forceinline__ void skinny_gemm_body(const GemmArgs& p, int n_blocks, int bid) {
   static_assert(NB == 2 || (!SWIGLU && NB == 1), "SwiGLU pairs a gate and an up block");
   static_assert(NW == 4 || NW == 8, "reduction written for 4 or 8 waves");
   // partial sums of the upper half of the waves (8 waves), then of waves 1..3
@@ -1090,12 +1092,12 @@ __global__ __launch_bounds__(64 * NW) void skinny_gemm_kernel(GemmArgs p, int n_
   if constexpr (kCanRoute) {
     if (p.rt_parts != nullptr) {
       routed = true;
-      skinny_route_prologue(p, rt_mask, rt_off, rt_tok, lane, wave);
+      skinny_route_prologue(p, rt_mask, rt_off, rt_tok, lane, wave, bid == 0);
     }
   }
   auto group_offset = [&](int i) { return routed ? rt_off[i] : p.offsets[i]; };
-  int g = blockIdx.x / n_blocks;
-  const int nb = blockIdx.x - g * n_blocks;
+  int g = bid / n_blocks;
+  const int nb = bid - g * n_blocks;
   int mb = 0, me = p.M;
   if (p.offsets != nullptr) {
     // The grid holds n_blocks workgroups for each of min(G, M) group ordinals
@@ -1352,6 +1354,11 @@ __global__ __launch_bounds__(64 * NW) void skinny_gemm_kernel(GemmArgs p, int n_
   }
 }
 
+template <int MT, bool SWIGLU, bool GATHER, bool TILED, int NB = 2, int NW = kSkinnyWaves>
+__global__ __launch_bounds__(64 * NW) void skinny_gemm_kernel(GemmArgs p, int n_blocks) {
+  skinny_gemm_body<MT, SWIGLU, GATHER, TILED, NB, NW>(p, n_blocks, blockIdx.x);
+}
+
 // Zero the output rows that no group covers: [0, offsets[0]) and [offsets[G], M).
 __global__ __launch_bounds__(256) void zero_uncovered_rows_kernel(
     uint16_t* __restrict__ C, int64_t ldc, int M, int N,
@@ -1439,8 +1446,10 @@ template <int MT, bool SWIGLU, bool GATHER, bool TILED>
 static int launch_skinny_gemm(const GemmArgs& a, hipStream_t st) {
   // groups: by offsets, or a batch of G equal groups of M rows (per-group bases)
   const int G = a.offsets != nullptr || a.a_group_stride != 0 || a.c_group_stride != 0 ? a.G : 1;
-  // group ordinals launched: with offsets, at most one busy group per row
-  const int64_t GL = a.offsets != nullptr ? std::min<int64_t>(G, std::max(a.M, 1)) : G;
+  // group ordinals launched: with non-decreasing offsets, at most one busy
+  // group per row; offsets from a caller may overlap, so every group gets one
+  const int64_t GL = a.offsets != nullptr && a.offsets_sorted
+                         ? std::min<int64_t>(G, std::max(a.M, 1)) : G;
   if constexpr (!SWIGLU) {
     // Few groups with rows (a decode step's projections: one group, one token):
     // 32-row blocks and 8 waves per workgroup, so the weights stream through

@@ -515,6 +515,22 @@ extern "C" size_t dsk_mla_decode_workspace_size(int batch, int q_len, int kv_len
   return align_up((size_t)batch * q_len * per_token, 256);
 }
 
+namespace dsk {
+// Whether two cache views of `wa` and `wb` columns per token row, with the same
+// token and batch strides (elements), share an element: disjoint extents never
+// do; inside one buffer the column offset of b relative to a's row start decides
+// (token rows of the same width repeat every ld elements).
+static bool rows_overlap(const dsk_bf16* a, int wa, const dsk_bf16* b, int wb, int64_t ld,
+                         int64_t ld_batch, int batch, int kv_len) {
+  const int64_t span = (int64_t)(batch - 1) * ld_batch + (int64_t)(kv_len - 1) * ld;
+  const int64_t d = b - a;  // elements
+  if (d >= span + wa || -d >= span + wb) return false;  // disjoint extents
+  if (ld_batch % ld != 0) return true;                  // cannot reason per row: refuse
+  const int64_t c = ((d % ld) + ld) % ld;               // b's column in a's row frame
+  return c < wa || c + wb > ld;
+}
+}  // namespace dsk
+
 extern "C" int dsk_mla_decode_attention(const dsk_bf16* q_abs, int64_t qa_tok, int64_t qa_head,
                                         const dsk_bf16* q_pe, int64_t qp_tok, int64_t qp_head,
                                         const dsk_bf16* latent, const dsk_bf16* k_pe,
@@ -554,6 +570,14 @@ extern "C" int dsk_mla_decode_attention(const dsk_bf16* q_abs, int64_t qa_tok, i
               "mla_decode_attention: inputs must be 16-byte aligned, the output 4-byte aligned");
   DSK_REQUIRE((int64_t)batch * q_len <= 65535, DSK_ERR_INVALID_ARG,
               "mla_decode_attention: batch * q_len must be <= 65535");
+  // k_rope is written by the kernel: it must not overlap the latent or k_pe rows
+  // it is read beside. Views sharing one buffer (the same strides) overlap where
+  // their column ranges meet inside a token row.
+  DSK_REQUIRE(!rows_overlap(k_rope, kRope, latent, kLat, ld_tok, ld_batch, batch, kv_len) &&
+                  !rows_overlap(k_rope, kRope, k_pe, kRope, ld_tok, ld_batch, batch, kv_len),
+              DSK_ERR_INVALID_ARG,
+              "mla_decode_attention: k_rope overlaps latent or k_pe (it is written while they "
+              "are read)");
   DSK_REQUIRE(bytes >= dsk_mla_decode_workspace_size(batch, q_len, kv_len), DSK_ERR_WORKSPACE,
               "mla_decode_attention: workspace too small");
   int S, per;

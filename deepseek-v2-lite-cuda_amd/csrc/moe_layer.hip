@@ -116,6 +116,7 @@ static int layer_after_gate(const float* logits, int n_parts, int64_t part_strid
   g1.C = h; g1.ldc = I;
   g1.offsets = offsets; g1.G = G;
   g1.M = Stot; g1.N = I; g1.K = H;
+  g1.offsets_sorted = 1;  // the route kernels' offsets never decrease
   g1.up_row_offset = I;
   g1.max_group_rows = T;  // a token routes to an expert at most once; shared groups hold T
   g1.b_tiled = weight_layout == DSK_LAYOUT_TILED;
@@ -144,6 +145,7 @@ static int layer_after_gate(const float* logits, int n_parts, int64_t part_strid
   g2.C = y; g2.ldc = H;
   g2.offsets = offsets; g2.G = G;
   g2.M = Stot; g2.N = H; g2.K = I;
+  g2.offsets_sorted = 1;
   g2.max_group_rows = T;
   g2.b_tiled = weight_layout == DSK_LAYOUT_TILED;
   if ((rc = run_gemm(g2, false, st))) return rc;
@@ -288,6 +290,18 @@ static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
 static std::atomic<void*> g_scratch_addr[kNoAllocMaxDevices];
 static std::mutex g_scratch_mu;
 
+// In-flight tracking of each GPU's scratch: an event recorded on the stream of
+// the last eager call after its kernels. A call on another stream of that GPU
+// while the event is pending would share the scratch with a running layer, so
+// it is refused (calls on one stream are ordered by the stream itself).
+struct NoAllocInFlight {
+  std::mutex mu;
+  hipEvent_t done = nullptr;
+  hipStream_t stream = nullptr;
+  bool recorded = false;
+};
+static NoAllocInFlight g_inflight[kNoAllocMaxDevices];
+
 // Device address of `scratch` on device `dev` (which must be current).
 static int scratch_address(int dev, void** out) {
   void* p = g_scratch_addr[dev].load(std::memory_order_acquire);
@@ -337,9 +351,41 @@ extern "C" int dsk_moe_layer_forward_noalloc(const dsk_bf16* x, const dsk_bf16* 
     DSK_REQUIRE(hipStreamGetDevice(st, &sdev) == hipSuccess && sdev == dev, DSK_ERR_INVALID_ARG,
                 "moe_layer_noalloc: the stream must belong to the current device");
   }
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  DSK_REQUIRE(hipStreamIsCapturing(st, &capture) == hipSuccess, DSK_ERR_LAUNCH,
+              "moe_layer_noalloc: hipStreamIsCapturing failed");
+  const bool eager = capture == hipStreamCaptureStatusNone;
+  NoAllocInFlight& fl = g_inflight[dev];
+  std::lock_guard<std::mutex> lock(fl.mu);
+  if (fl.done == nullptr) {
+    // one-time set-up per device (the scratch address and the in-flight event)
+    // is not capturable: the first call on a device must be an eager one
+    DSK_REQUIRE(eager, DSK_ERR_INVALID_ARG,
+                "moe_layer_noalloc: the first call on a device must not be under stream "
+                "capture (it resolves the device's scratch); make one eager call first");
+    DSK_REQUIRE(hipEventCreateWithFlags(&fl.done, hipEventDisableTiming) == hipSuccess,
+                DSK_ERR_LAUNCH, "moe_layer_noalloc: hipEventCreate failed");
+  }
   void* ws = nullptr;
   if ((rc = scratch_address(dev, &ws))) return rc;
-  return dsk_moe_layer_forward(x, gate_weight, gate_bias, w1, w2, out, T, E, K, nsh, H, I,
-                               weight_layout, topk_idx_out, topk_w_out, expert_offsets_out, ws,
-                               kNoAllocScratchBytes, stage_events, stream);
+  if (eager && fl.recorded && fl.stream != st) {
+    const hipError_t q = hipEventQuery(fl.done);
+    DSK_REQUIRE(q != hipErrorNotReady, DSK_ERR_INVALID_ARG,
+                "moe_layer_noalloc: a call on another stream of this GPU is still running; "
+                "the static scratch is shared by every call on a GPU, so calls on different "
+                "streams must be serialised (or use dsk_moe_layer_forward with a workspace)");
+    DSK_REQUIRE(q == hipSuccess, DSK_ERR_LAUNCH,
+                std::string("moe_layer_noalloc: hipEventQuery failed: ") + hipGetErrorString(q));
+  }
+  rc = dsk_moe_layer_forward(x, gate_weight, gate_bias, w1, w2, out, T, E, K, nsh, H, I,
+                             weight_layout, topk_idx_out, topk_w_out, expert_offsets_out, ws,
+                             kNoAllocScratchBytes, stage_events, stream);
+  if (rc) return rc;
+  if (eager) {
+    DSK_REQUIRE(hipEventRecord(fl.done, st) == hipSuccess, DSK_ERR_LAUNCH,
+                "moe_layer_noalloc: hipEventRecord failed");
+    fl.stream = st;
+    fl.recorded = true;
+  }
+  return DSK_OK;
 }

@@ -84,4 +84,86 @@ __device__ __forceinline__ void route_token(const float* __restrict__ logits, in
   }
 }
 
+
+// Routing of one chunk of kRouteChunk tokens by one workgroup, four tokens per
+// wave (one per 16-lane row; the workgroup needs a wave per four tokens of the
+// chunk). Writes topk idx / weights, the chunk histogram, and (optionally) each
+// (token, k)'s rank inside its chunk. With a single chunk (T <= 64) it also
+// finishes the job that the scan and permutation kernels do for larger T:
+// counts, offsets (including the rows of the always-on groups appended after
+// the routed ones), token_map and slot_of.
+constexpr int kRouteChunk = 64;  // tokens per routing workgroup (= mask width)
+
+__device__ __forceinline__ void route_chunk_body(
+    const float* __restrict__ logits, int64_t ld, int n_parts, int64_t part_stride,
+    const float* __restrict__ bias, int T, int E, int K,
+    int32_t* __restrict__ topk_idx, float* __restrict__ topk_w,
+    int32_t* __restrict__ blk_hist, int32_t* __restrict__ local_rank,
+    int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ token_map, int32_t* __restrict__ slot_of,
+    int n_extra_groups, int chunk, bool single_chunk) {
+  __shared__ unsigned long long s_mask[64];
+  __shared__ int s_off[64];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  if (tid < 64) s_mask[tid] = 0ull;
+  __syncthreads();
+
+  const int t0 = chunk * kRouteChunk;
+  // Four tokens per wave at once: the 16 lanes of row g hold token
+  // tl = 4 * wave + g (route_token).
+  const int g = lane >> 4, j = lane & 15;
+  const int tl = 4 * wave + g;
+  const int t = t0 + tl;
+  const bool active = t < T;  // uniform over the 16-lane row
+  // waves whose four rows are all past T skip the selection
+  const bool wave_active = t0 + 4 * wave < T;
+  int my_e;
+  float my_w;
+  route_token(logits, ld, n_parts, part_stride, bias, t, active, wave_active, E, K, lane, my_e,
+              my_w);
+  if (active && j < K) {
+    topk_idx[(int64_t)t * K + j] = my_e;
+    topk_w[(int64_t)t * K + j] = my_w;
+    atomicOr(&s_mask[my_e], 1ull << tl);
+  } else {
+    my_e = -1;
+  }
+  __syncthreads();
+
+  if (blk_hist != nullptr && tid < E)
+    blk_hist[(int64_t)chunk * E + tid] = __popcll(s_mask[tid]);
+
+  const int rank = my_e >= 0 ? __popcll(s_mask[my_e] & ((1ull << tl) - 1ull)) : -1;
+  if (local_rank != nullptr && my_e >= 0) local_rank[(int64_t)t * K + j] = rank;
+
+  if (single_chunk && offsets != nullptr) {
+    if (wave == 0) {
+      const int c = lane < E ? __popcll(s_mask[lane]) : 0;
+      const int inc = wave_inclusive_scan(c);
+      if (lane < E) {
+        offsets[lane] = inc - c;
+        s_off[lane] = inc - c;
+        if (counts != nullptr) counts[lane] = c;
+      }
+      if (lane == 63) {
+        offsets[E] = inc;
+        for (int x = 1; x <= n_extra_groups; ++x) offsets[E + x] = inc + x * T;
+      }
+    }
+    if (token_map != nullptr) {
+      __syncthreads();
+      if (my_e >= 0) {
+        const int slot = s_off[my_e] + rank;
+        token_map[slot] = t;
+        if (slot_of != nullptr) slot_of[(int64_t)t * K + j] = slot;
+      }
+      // rows of the always-on groups: group E+x row t is token t
+      const int S = T * K;
+      for (int r = tid; r < n_extra_groups * T; r += blockDim.x) token_map[S + r] = r % T;
+    }
+  }
+}
+
 }  // namespace dsk

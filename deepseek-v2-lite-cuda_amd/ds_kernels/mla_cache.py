@@ -38,6 +38,12 @@ class LatentKVCache:
     k_pe_cache [bsz, max_seq, rope_head_dim]  raw shared RoPE key, a view
     k_rope     [bsz, max_seq, rope_head_dim]  the RoPE key after RoPE (positions
                                               < rope_len hold it), a view
+
+    The rotated keys are valid for the cos/sin tensors that produced them: a
+    decode step given other table tensors rotates every cached key again. A
+    caller that writes kv_latent or k_pe_cache directly (not through update()
+    or a decode step) must call reset_rope() (or reset()) afterwards, or the
+    rotated keys of the rewritten positions stay stale.
     """
 
     def __init__(self, bsz: int, max_seq: int, kv_lora_rank: int = 512, rope_head_dim: int = 64,
@@ -54,6 +60,7 @@ class LatentKVCache:
         self.dtype = dtype
         self._len = 0
         self._rope_len = 0   # leading positions whose k_rope is valid
+        self._rope_tables = None   # identity of the cos/sin tables that rotated them
         w = kv_lora_rank + rope_head_dim
         self.rows = torch.zeros((bsz, max_seq, w + rope_head_dim), dtype=dtype,
                                 device=self.device)
@@ -129,6 +136,20 @@ class LatentKVCache:
         """Start a new sequence; keeps the buffers (mla_cache.py:171-176)."""
         self._len = 0
         self._rope_len = 0
+
+    def reset_rope(self) -> None:
+        """Mark every rotated key stale (after direct writes into kv_latent or
+        k_pe_cache): the next decode step rotates them again."""
+        self._rope_len = 0
+
+    def use_rope_tables(self, cos: torch.Tensor, sin: torch.Tensor) -> None:
+        """Called by a decode step with its tables: rotated keys made with other
+        tables (another tensor, or these modified in place) are dropped."""
+        key = (cos.data_ptr(), sin.data_ptr(), tuple(cos.shape), tuple(sin.shape), cos.dtype,
+               sin.dtype, cos._version, sin._version)
+        if key != self._rope_tables:
+            self._rope_len = 0
+            self._rope_tables = key
 
     def __repr__(self) -> str:
         used = (self._len * (self.kv_lora_rank + self.rope_head_dim) * self.rows.element_size()
@@ -246,6 +267,7 @@ def mla_decode_forward(x: torch.Tensor, W: MLAWeights, cache: LatentKVCache, cos
              f"KV cache overflow: current_len={cache.current_len}, new_tokens={n}, "
              f"max_seq={cache.max_seq}. Increase max_seq or reset the cache.")
     A = absorbed if absorbed is not None else AbsorbedMLAWeights.from_mla(W)
+    cache.use_rope_tables(cos, sin)
     len0 = cache.current_len
     rows = cache.append_slots(n)                           # [b, n, 576] slots
     try:

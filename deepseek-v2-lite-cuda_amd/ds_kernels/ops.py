@@ -644,6 +644,24 @@ def mla_attn_pack(q: torch.Tensor, kv: torch.Tensor, k_pe: torch.Tensor, cos: to
     return q_out, k_t, v
 
 
+def _rows_overlap(a: torch.Tensor, wa: int, b: torch.Tensor, wb: int) -> bool:
+    """Whether views a and b ([bsz, L, w] with the same batch and token strides)
+    share an element: separate storages never do; inside one buffer, b's column
+    offset within a's token row decides."""
+    if a.untyped_storage().data_ptr() != b.untyped_storage().data_ptr():
+        return False
+    ld, lb = a.stride(1), a.stride(0)
+    B, L = a.shape[0], a.shape[1]
+    span = (B - 1) * lb + (L - 1) * ld
+    d = b.storage_offset() - a.storage_offset()
+    if d >= span + wa or -d >= span + wb:
+        return False
+    if B > 1 and lb % ld != 0:
+        return True
+    c = d % ld
+    return c < wa or c + wb > ld
+
+
 def mla_decode_attention(q_abs: torch.Tensor, q_pe: torch.Tensor, latent: torch.Tensor,
                          k_pe: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, scale: float,
                          eps: float = 1e-6, out: torch.Tensor = None,
@@ -658,8 +676,12 @@ def mla_decode_attention(q_abs: torch.Tensor, q_pe: torch.Tensor, latent: torch.
     [bsz, L, 64] with the same strides, the keys after RoPE: rows < rope_len
     are read, rows from rope_len on are rotated from k_pe and written (None: a
     scratch buffer, every key rotated here). All may be strided views with a
-    contiguous last dim. Returns bf16 [T, 16, 512] (into `out` if given):
-    sum_j softmax_j r_j x_j per head."""
+    contiguous last dim; k_rope must not overlap latent or k_pe. Without k_rope
+    the op allocates a scratch of the latent's strides (up to bsz x token
+    stride x L elements, of which it writes 64 per token) and rotates all L
+    keys on every call; LatentKVCache.k_rope keeps them across calls instead.
+    Returns bf16 [T, 16, 512] (into `out` if given): sum_j softmax_j r_j x_j
+    per head."""
     op = "mla_decode_attention"
     for t, nm in ((q_abs, "q_abs"), (q_pe, "q_pe"), (latent, "latent"), (k_pe, "k_pe"),
                   (cos, "cos"), (sin, "sin")):
@@ -675,14 +697,21 @@ def mla_decode_attention(q_abs: torch.Tensor, q_pe: torch.Tensor, latent: torch.
     _req(latent.stride()[:2] == k_pe.stride()[:2],
          f"{op}: latent and k_pe must share batch and token strides.")
     if k_rope is None:
-        rows = torch.empty((b, L, 640), dtype=torch.bfloat16, device=latent.device)
-        rows[..., :512].copy_(latent)
-        rows[..., 512:576].copy_(k_pe)
-        latent, k_pe, k_rope, rope_len = rows[..., :512], rows[..., 512:576], rows[..., 576:], 0
+        # scratch for the rotated keys with the latent's strides (the kernel
+        # addresses all three by one token stride); only its 64 columns per
+        # token are written, every key rotated here (rope_len 0)
+        sb, st_ = latent.stride(0), latent.stride(1)
+        extent = (b - 1) * sb + (L - 1) * st_ + 64
+        k_rope = torch.empty(extent, dtype=torch.bfloat16,
+                             device=latent.device).as_strided((b, L, 64), (sb, st_, 1))
+        rope_len = 0
     _req(isinstance(k_rope, torch.Tensor) and k_rope.is_cuda and k_rope.dtype == torch.bfloat16
          and k_rope.shape == (b, L, 64) and k_rope.stride()[:2] == latent.stride()[:2]
          and k_rope.stride(-1) == 1,
          f"{op}: k_rope must be bf16 [bsz, L, 64] with the strides of latent.")
+    for t, nm, w in ((latent, "latent", 512), (k_pe, "k_pe", 64)):
+        _req(not _rows_overlap(k_rope, 64, t, w),
+             f"{op}: k_rope overlaps {nm} (it is written while {nm} is read).")
     _req(isinstance(rope_len, int) and 0 <= rope_len <= L, f"{op}: need 0 <= rope_len <= {L}.")
     _req(b > 0 and T % b == 0, f"{op}: T={T} is not a multiple of bsz={b}.")
     n = T // b

@@ -470,10 +470,14 @@ int dsk_moe_layer_forward(const dsk_bf16* x, const dsk_bf16* gate_weight,
  * DSK_NOALLOC_SCRATCH_BYTES are rejected with DSK_ERR_WORKSPACE (at the
  * DeepSeek-V2-Lite shapes E=64, K=6, 2 shared groups, H=2048, I=1408 that
  * admits T <= 128, the decode sizes). The stream must belong to the current
- * device; the first call on a device resolves the array's device address.
- * Every call on one GPU shares that GPU's array (no state is carried from one
- * call to the next): calls that overlap on one GPU, e.g. on two streams, race
- * and must be serialised by the caller. Arguments otherwise as for
+ * device. The first call on a device must be eager (not under stream capture):
+ * it resolves the array's device address and creates the device's in-flight
+ * event; later calls may be captured into a HIP graph. Every call on one GPU
+ * shares that GPU's array (no state is carried from one call to the next), so
+ * calls that overlap on one GPU would race: an eager call on another stream
+ * while the previous eager call is still running is refused with
+ * DSK_ERR_INVALID_ARG; captured calls are not tracked, and replays of graphs
+ * holding them must be serialised by the caller. Arguments otherwise as for
  * dsk_moe_layer_forward. */
 #define DSK_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
 int dsk_moe_layer_forward_noalloc(const dsk_bf16* x, const dsk_bf16* gate_weight,

@@ -215,9 +215,12 @@ def test_mla_decode_validation(dsk):
     # argument order: q_abs, qa_tok, qa_head, q_pe, qp_tok, qp_head, latent, k_pe, k_rope,
     # rope_len, ld_tok, ld_batch, cos, sin, eps, scale, batch, q_len, kv_len, out, o_tok,
     # o_head, ws, bytes, stream
+    # one 640-wide cache row per token: latent at column 0, k_pe at 512, k_rope at 576
+    lat, kpe, krope = 1 << 20, (1 << 20) + 1024, (1 << 20) + 1152
+
     def call(q_len=1, kv_len=64, ld_tok=640, ld_batch=640 * 64, batch=1, qa=(8192, 512),
-             out=16, bytes_=1 << 30, q_abs=16, k_rope=16, rope_len=0):
-        return lib.dsk_mla_decode_attention(q_abs, qa[0], qa[1], 16, 3072, 192, 16, 16, k_rope,
+             out=16, bytes_=1 << 30, q_abs=16, k_rope=krope, rope_len=0):
+        return lib.dsk_mla_decode_attention(q_abs, qa[0], qa[1], 16, 3072, 192, lat, kpe, k_rope,
                                             rope_len, ld_tok, ld_batch, 16, 16, 1e-6, 0.1, batch,
                                             q_len, kv_len, out, 8192, 512, 16, bytes_, None)
     assert lib.dsk_mla_decode_attention(None, 0, 0, None, 0, 0, None, None, None, 0, 0, 0, None,
@@ -236,6 +239,14 @@ def test_mla_decode_validation(dsk):
     assert call(out=18) == 3
     assert call(kv_len=4096, bytes_=1024) == 5 and "workspace" in _err(dsk)
     assert call(batch=256, q_len=256, kv_len=256, ld_batch=640 * 256) == 1 and "65535" in _err(dsk)
+    # k_rope is written while latent and k_pe are read: overlapping views are refused
+    assert call(k_rope=kpe) == 1 and "overlaps" in _err(dsk)
+    assert call(k_rope=lat + 512) == 1 and "overlaps" in _err(dsk)
+    assert call(k_rope=lat + 1280 * 2, ld_tok=1280, ld_batch=1280 * 64) == 1  # next row's latent
+    # columns 640..703 of 1280-wide rows: clear of both (stops at the workspace check)
+    assert call(k_rope=lat + 1280 * 3, ld_tok=1280, ld_batch=1280 * 64, kv_len=4096,
+                bytes_=1024) == 5
+    assert call(k_rope=1 << 30, kv_len=4096, bytes_=1024) == 5  # a separate buffer
 
 
 def test_linear_batched_validation(dsk):

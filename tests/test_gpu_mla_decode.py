@@ -98,6 +98,43 @@ def test_decode_prompt_longer_than_4096(setup):
     assert max_rel_err(np32(out[:, S - 1:]), ref[:, S - 1:]) <= BF16_TOL
 
 
+def test_decode_step_with_new_tables_rotates_again(setup):
+    """Keys rotated with one pair of tables are not reused with another: a step
+    given new tables equals the same step on a fresh cache filled with the new
+    tables, bit for bit."""
+    dsk, W, A, wn, cos, sin = setup
+    cos2, sin2 = torch.roll(cos, 3, 0).contiguous(), torch.roll(sin, 3, 0).contiguous()
+    g = torch.Generator().manual_seed(91)
+    x = torch.randn(1, 40, 2048, generator=g).to(torch.bfloat16).to(DEV)
+    c1 = dsk.LatentKVCache(1, 64, device=DEV)
+    dsk.mla_decode_forward(x[:, :39], W, c1, cos, sin, A)
+    o1 = dsk.mla_decode_forward(x[:, 39:], W, c1, cos2, sin2, A)
+    c2 = dsk.LatentKVCache(1, 64, device=DEV)
+    dsk.mla_decode_forward(x[:, :39], W, c2, cos2, sin2, A)
+    o2 = dsk.mla_decode_forward(x[:, 39:], W, c2, cos2, sin2, A)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
+
+
+def test_decode_attention_rejects_overlapping_k_rope(setup):
+    """k_rope is written while latent and k_pe are read: a k_rope view on the
+    raw keys (a natural 'rotate in place' call) is refused before any launch."""
+    dsk, W, A, wn, cos, sin = setup
+    rows = torch.randn(1, 16, 640).to(torch.bfloat16).to(DEV)
+    q_abs = torch.zeros(1, 16, 512, dtype=torch.bfloat16, device=DEV)
+    q_pe = torch.zeros(1, 16, 64, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match="overlaps"):
+        dsk.mla_decode_attention(q_abs, q_pe, rows[..., :512], rows[..., 512:576], cos, sin,
+                                 0.1, k_rope=rows[..., 512:576])
+    with pytest.raises(RuntimeError, match="overlaps"):
+        dsk.mla_decode_attention(q_abs, q_pe, rows[..., :512], rows[..., 512:576], cos, sin,
+                                 0.1, k_rope=rows[..., 448:512])
+    out = dsk.mla_decode_attention(q_abs, q_pe, rows[..., :512], rows[..., 512:576], cos, sin,
+                                   0.1)       # scratch keys: no overlap
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out.float()).all())
+
+
 def test_cache_holds_raw_projection_rows(setup):
     """The cache stores kv_a_proj_with_mqa's raw output (pre-norm latent,
     pre-RoPE key), as mla_cache.py:33-35 documents."""

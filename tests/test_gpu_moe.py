@@ -242,6 +242,27 @@ def test_gemm_small_groups(dsk, counts):
     assert max_rel_err(np32(out2), om.grouped_linear(np32(h), np32(w2), off)) <= BF16_TOL
 
 
+def test_gemm_small_groups_caller_offsets_not_sorted(dsk):
+    """Offsets from a caller need not increase: here busy groups (3) outnumber
+    the rows (2), group 4 alone covers row 1, and groups 0, 2 and 4 (identical
+    weights) all cover row 0. Every busy group must run on the small-group
+    path (none dropped), so both rows equal x @ W^T (the reference loops over
+    every expert's range, gemm1.cu:94-123)."""
+    g = torch.Generator().manual_seed(77)
+    H, N = 2048, 2816
+    a = torch.randn(2, H, generator=g).to(torch.bfloat16)
+    w0 = (torch.randn(N, H, generator=g) * 0.02).to(torch.bfloat16)
+    w = torch.stack([w0 if e % 2 == 0 else torch.zeros_like(w0) for e in range(5)])
+    off = torch.tensor([0, 1, 0, 1, 0, 2], dtype=torch.int32)
+    out = dsk.moe_gemm1(a.to(DEV), w.to(DEV), off.to(DEV))
+    ref = np32(a) @ np32(w0).T
+    assert max_rel_err(np32(out), ref) <= BF16_TOL
+    out2 = dsk.moe_gemm2(a[:, :1408].contiguous().to(DEV), w[:, :, :1408].contiguous().to(DEV),
+                         off.to(DEV))
+    ref2 = np32(a[:, :1408]) @ np32(w0[:, :1408]).T
+    assert max_rel_err(np32(out2), ref2) <= BF16_TOL
+
+
 def test_gemm_zero_slots(dsk):
     out = dsk.moe_gemm1(torch.empty(0, 2048, dtype=torch.bfloat16, device=DEV),
                         torch.zeros(64, 2816, 2048, dtype=torch.bfloat16, device=DEV),

@@ -147,3 +147,29 @@ def test_rejected_decode_step_leaves_the_cache_length():
     with pytest.raises(RuntimeError, match="CUDA"):
         mla_decode_forward(x, W, c, cos, sin)
     assert c.current_len == 5
+
+
+def test_rope_tables_identity_and_reset_rope():
+    """Rotated keys belong to the tables that made them: other tables (or the
+    same tensor modified in place) drop them, reset_rope() drops them after
+    direct writes into the planes."""
+    c = LatentKVCache(1, 8, kv_lora_rank=16, rope_head_dim=8, device="cpu")
+    c.update(torch.zeros(1, 4, 16), torch.zeros(1, 4, 8))
+    cos, sin = torch.ones(8, 8), torch.zeros(8, 8)
+    c.use_rope_tables(cos, sin)
+    c._rope_len = 4                      # as a decode step leaves it
+    c.use_rope_tables(cos, sin)          # same tables: kept
+    assert c.rope_len == 4
+    c.use_rope_tables(cos.clone(), sin)  # another tensor: dropped
+    assert c.rope_len == 0
+    c._rope_len = 4
+    c.use_rope_tables(cos, sin)          # back to the first tensor: also new
+    assert c.rope_len == 0
+    c._rope_len = 4
+    cos.mul_(2)                          # modified in place
+    c.use_rope_tables(cos, sin)
+    assert c.rope_len == 0
+    c._rope_len = 4
+    c.k_pe_cache[:, :2] = 1.0            # direct write into the raw keys
+    c.reset_rope()
+    assert c.rope_len == 0 and c.current_len == 4
