@@ -23,7 +23,7 @@ Also reported on the same line:
                 reported value) and config 0 (T=64) beside it.
 
 Usage: python bench.py [--gpus 1] [--steps K (200)] [--warmup W (20)]
-                       [--profile | --decode-only T | --mla-only | --mla-decode-only]
+                       [--profile | --decode-only T | --mla-only | --mla-decode-only | --ramp]
 """
 from __future__ import annotations
 
@@ -168,6 +168,57 @@ def bench_decode(dsk, syn, torch, F, W, packed, T, steps, ev, copies):
             "us_per_step_graph_replay": med_graph * 1e3,
             "timing": "median of 50 eager steps, HIP events on the launch stream",
             "algorithmic_bytes": bytes_, "GB/s": gbs, "frac_of_8TB/s": gbs / PEAK_HBM_GBS}
+
+
+def ramp_probe(dsk, syn, torch, W, packed, ev, n=60):
+    """Per-step times of the T=4096 layer right after the set-up (no warm-up), then,
+    after one idle second each: 40 launches of a 512 MB device copy (HBM only),
+    40 of a dense 8192^3 bf16 product (matrix cores only) and 30 more layer
+    steps. A core-clock ramp slows the product and the layer, not the copy."""
+    w1, w2, nsh = packed
+    dev = w1.device
+    wg = dsk.tile_weights(W.wg.to(torch.bfloat16)[None])[0].to(dev)
+    x = syn.tokens(4096).to(torch.bfloat16).to(dev)
+    ws = torch.empty(dsk.lib.dsk_moe_layer_workspace_size(4096, 64, 6, nsh, 2048, 1408),
+                     dtype=torch.uint8, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+
+    def layer_steps(k):
+        evs = [ev.create(5) for _ in range(k)]
+        for e in evs:
+            dsk.moe_layer_forward(x, wg, w1, w2, 6, nsh, workspace=ws, stage_events=e)
+        torch.cuda.synchronize()
+        out = [[ev.ms(e[j], e[j + 1]) * 1e3 for j in range(4)] for e in evs]
+        for e in evs:
+            ev.destroy(e)
+        return out
+
+    def launches(fn, k):
+        evs = ev.create(2 * k)
+        for i in range(k):
+            ev.rt.hipEventRecord(evs[2 * i], st)
+            fn()
+            ev.rt.hipEventRecord(evs[2 * i + 1], st)
+        torch.cuda.synchronize()
+        out = [ev.ms(evs[2 * i], evs[2 * i + 1]) * 1e3 for i in range(k)]
+        ev.destroy(evs)
+        return out
+
+    res = {"layer_steps_after_setup_us": layer_steps(n)}
+    src = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    a = torch.randn(8192, 8192, device=dev, dtype=torch.bfloat16)
+    b = torch.randn(8192, 8192, device=dev, dtype=torch.bfloat16)
+    c = torch.empty_like(a)
+    torch.mm(a, b, out=c)
+    torch.cuda.synchronize()
+    time.sleep(1.0)
+    res["copy_512MB_after_idle_us"] = launches(lambda: dst.copy_(src), 40)
+    time.sleep(1.0)
+    res["mm_8192_bf16_after_idle_us"] = launches(lambda: torch.mm(a, b, out=c), 40)
+    time.sleep(1.0)
+    res["layer_steps_after_idle_us"] = layer_steps(30)
+    return res
 
 
 def graph_timer(torch, ev, reps=20, warmup=5):
@@ -488,6 +539,9 @@ def main():
                     help="only the MLA projection block and decoder layer (for profiling)")
     ap.add_argument("--mla-decode-only", action="store_true",
                     help="only the latent-cache decode attention and decode step (for profiling)")
+    ap.add_argument("--ramp", action="store_true",
+                    help="per-step layer times from a cold start, and a copy and a dense product "
+                         "after an idle second (the clock ramp)")
     args = ap.parse_args()
     if args.calibrate_copy:
         calibrate_copy(3)
@@ -522,6 +576,10 @@ def main():
     packed = (dsk.tile_weights(w1), dsk.tile_weights(w2), nsh)
     del w1, w2
     ev = HipEvents()
+
+    if args.ramp:
+        print(json.dumps(ramp_probe(dsk, syn, torch, W, packed, ev)), flush=True)
+        return
 
     if args.decode_only:
         w1, w2, nsh = packed
