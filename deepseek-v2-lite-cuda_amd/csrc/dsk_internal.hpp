@@ -82,6 +82,11 @@ int launch_route(const float* logits, int64_t ld, int n_parts, int64_t part_stri
 // Partial gate sums: parts[s][t][e] = sum over the s-th of n_parts K slices of
 // x[t, k] * wg[e, k] (fp32), for the route kernel to add up.
 int gate_parts_count(int T, int E, int H);
+// Full gate logits (16 waves per 32 x 32 block, K split over the waves and
+// reduced in the LDS in a fixed order), + bias[e] if bias is not NULL.
+int launch_gate_logits(const uint16_t* x, int64_t ld_x, const uint16_t* wg, bool tiled,
+                       const float* bias, float* logits, int64_t ld_out, int T, int E, int H,
+                       hipStream_t st);
 int launch_gate_parts(const uint16_t* x, int64_t ld_x, const uint16_t* wg, bool tiled,
                       float* parts, int T, int E, int H, int n_parts, hipStream_t st);
 int launch_scan(const int32_t* hist, int nblk, int E, int32_t* counts, int32_t* offsets,

@@ -118,6 +118,16 @@ int gate_parts_count(int T, int E, int H) {
   return n > H / 16 ? H / 16 : n;
 }
 
+int launch_gate_logits(const uint16_t* x, int64_t ld_x, const uint16_t* wg, bool tiled,
+                       const float* bias, float* logits, int64_t ld_out, int T, int E, int H,
+                       hipStream_t st) {
+  dim3 grid((T + 31) / 32, (E + 31) / 32);
+  auto kern = tiled ? gate_logits_kernel<true> : gate_logits_kernel<false>;
+  hipLaunchKernelGGL(kern, grid, dim3(64 * kGateWaves), 0, st, x, ld_x, wg, bias, logits, ld_out,
+                     T, E, H);
+  return check_launch("gate_logits_kernel");
+}
+
 int launch_gate_parts(const uint16_t* x, int64_t ld_x, const uint16_t* wg, bool tiled,
                       float* parts, int T, int E, int H, int n_parts, hipStream_t st) {
   dim3 grid((T + 31) / 32, (E + 31) / 32, n_parts);
@@ -149,12 +159,8 @@ extern "C" int dsk_moe_gate_logits(const dsk_bf16* x, int64_t ld_x, const dsk_bf
               "moe_gate: x and gate_weight rows must be 16-byte aligned");
   DSK_REQUIRE(ld_x >= H && ld_logits >= E, DSK_ERR_INVALID_ARG,
               "moe_gate: row stride smaller than the row");
-  dim3 grid((T + 31) / 32, (E + 31) / 32);
-  auto kern = weight_layout == DSK_LAYOUT_TILED ? gate_logits_kernel<true>
-                                                : gate_logits_kernel<false>;
-  hipLaunchKernelGGL(kern, grid, dim3(64 * kGateWaves), 0, as_stream(stream),
-                     reinterpret_cast<const uint16_t*>(x), ld_x,
-                     reinterpret_cast<const uint16_t*>(gate_weight), bias, logits, ld_logits, T,
-                     E, H);
-  return check_launch("gate_logits_kernel");
+  return launch_gate_logits(reinterpret_cast<const uint16_t*>(x), ld_x,
+                            reinterpret_cast<const uint16_t*>(gate_weight),
+                            weight_layout == DSK_LAYOUT_TILED, bias, logits, ld_logits, T, E, H,
+                            as_stream(stream));
 }

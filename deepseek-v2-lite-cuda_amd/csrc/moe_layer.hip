@@ -264,6 +264,10 @@ extern "C" int dsk_moe_layer_forward(const dsk_bf16* x, const dsk_bf16* gate_wei
   const FusedLayout L = fused_layout(T, E, K, nsh, H, I);
   char* ws = static_cast<char*>(workspace);
   float* parts = reinterpret_cast<float*>(ws + layer_parts_offset(T, E, K, nsh, H, I));
+  // Partial sums over K slices in single-wave workgroups: at decode sizes they
+  // spread the gate weight's loads over the CUs, and at T=4096 the full logits
+  // (16 waves per 32 x 32 block reducing their K slices in the LDS, one plane)
+  // measured slower: gate + route 29.0 against 31.4 us.
   const int n_parts = gate_parts_count(T, E, H);
   rc = launch_gate_parts(x, H, gate_weight, weight_layout == DSK_LAYOUT_TILED, parts, T, E, H,
                          n_parts, st);
