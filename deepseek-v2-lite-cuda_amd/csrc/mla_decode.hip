@@ -50,7 +50,17 @@ namespace dsk {
 constexpr int kLat = 512;     // latent width
 constexpr int kRope = 64;     // RoPE key width
 constexpr int kHeads = 16;
-constexpr int kWaves = 4;
+constexpr int kWaves = 4;  // compute waves (16 keys each per block)
+// Waves that only issue the ring's DMA, beside the compute waves: a wave moves
+// about 10 GB/s through the memory pipeline however many loads it keeps in
+// flight, so 4 waves that also score and accumulate fetch a 75 KB block at
+// ~22 GB/s per CU; with the loads on 4 more waves (2 per SIMD) the compute
+// waves never stall on a full memory queue.
+#ifndef DSK_ATTN_PRODUCERS
+#define DSK_ATTN_PRODUCERS 4
+#endif
+constexpr int kProducers = DSK_ATTN_PRODUCERS;
+constexpr int kSplitThreads = 64 * (kWaves + kProducers);
 constexpr int kBlock = 64;                   // keys per block: 4 waves x 16
 constexpr int kMaxSplits = 256;              // key splits per query token
 // A stage of the ring, in 16-byte pieces: the block's 64 latent rows at a
@@ -153,7 +163,7 @@ __device__ __forceinline__ void lds_barrier_lgkm() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-__global__ __launch_bounds__(256, 1) void attn_split_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(kSplitThreads, 1) void attn_split_kernel(DecodeArgs a) {
   __shared__ __attribute__((aligned(1024))) char s_ring[kRingBytes];
   __shared__ __attribute__((aligned(16))) uint16_t s_p[kHeads][kPPitch];  // P'^T by slot
   __shared__ float s_max[4][kHeads], s_l[4][kHeads];
@@ -178,8 +188,10 @@ __global__ __launch_bounds__(256, 1) void attn_split_kernel(DecodeArgs a) {
   // instructions wave, wave + 4, wave + 8 (slot s = 64 r + l holds piece s % 9
   // of key s / 9; padding slots fetch piece 7). Rows past the cache are clamped
   // to its last row; their scores are masked.
+  // dw: the issuing wave's slot 0..3 (a compute wave, or a producer wave - 4)
+  const int dw = wave < kWaves ? wave : wave - kWaves;
   auto dma_lat = [&](int kb, uint32_t st, int j) __attribute__((always_inline)) {
-    const int row = 16 * wave + j;
+    const int row = 16 * dw + j;
     dma_ring(lat_b, (uint32_t)min(kb + row, L - 1) * ld_bytes + (uint32_t)(lane << 4),
              st + row * kLatPitch);
   };
@@ -192,7 +204,7 @@ __global__ __launch_bounds__(256, 1) void attn_split_kernel(DecodeArgs a) {
   auto dma_block = [&](int kb, uint32_t st) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) dma_lat(kb, st, j);
-    for (int r = wave; r < kRopeDma; r += 4) dma_rope(kb, st, r);
+    for (int r = dw; r < kRopeDma; r += 4) dma_rope(kb, st, r);
   };
 
   // ---- query: q_abs rows (16 heads at the latent row pitch), raw q_pe (2 KB)
@@ -201,7 +213,7 @@ __global__ __launch_bounds__(256, 1) void attn_split_kernel(DecodeArgs a) {
   const uint32_t q_lds = ring0 + kStageBytes;
   const uint32_t qp_lds = q_lds + kHeads * kLatPitch;           // [16][64] raw q_pe
   const uint32_t ang_lds = qp_lds + kHeads * kRope * 2;         // cos row; sin row 1 KB on
-  {
+  if (wave < kWaves) {
     const char* qa = reinterpret_cast<const char*>(a.q_abs + tok * a.qa_tok);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -217,10 +229,28 @@ __global__ __launch_bounds__(256, 1) void attn_split_kernel(DecodeArgs a) {
       dma_1kb(tab, (uint32_t)((int64_t)pos_q * kRope * 2 + (min(lane, 7) << 4)),
               ang_lds + (wave - 2) * 1024);
     }
-    if (n_blk > 0) dma_block(k_begin, ring0);
+    if (kProducers == 0 && n_blk > 0) dma_block(k_begin, ring0);
+  } else if (n_blk > 0) {
+    dma_block(k_begin, ring0);
   }
   wait_vmcnt<0>();
   lds_barrier();
+  if (kProducers > 0 && wave >= kWaves) {
+    // Producer: block i + 1's DMA right after the barrier that frees its stage,
+    // then the compute waves' two barriers of the block; the same barrier
+    // count as theirs, to the end.
+    for (int i = 0; i < n_blk; ++i) {
+      wait_vmcnt<0>();
+      lds_barrier();
+      if (i + 1 < n_blk) dma_block(k_begin + (i + 1) * kBlock, ring0 + ((i + 1) & 1) * kStageBytes);
+      lds_barrier_lgkm();  // s_max
+      lds_barrier_lgkm();  // s_p
+    }
+    wait_vmcnt<0>();
+    lds_barrier_lgkm();
+    if (a.n_splits == 1) lds_barrier_lgkm();
+    return;
+  }
   u32x4_t qv[kLat / 32], qr[2];  // scores operand B: head r16, dims 8g.. of each 32-dim step
 #pragma unroll
   for (int ks = 0; ks < kLat / 32; ++ks) qv[ks] = lds_read16(q_lds + r16 * kLatPitch + (4 * ks + g) * 16);
@@ -275,9 +305,9 @@ __global__ __launch_bounds__(256, 1) void attn_split_kernel(DecodeArgs a) {
       acc_n = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xa[ks]),
                                                       __builtin_bit_cast(bf16x8_t, qv[ks]),
                                                       acc_n, 0, 0, 0);
-      if (more) dma_lat(kb + kBlock, st_next, ks);
+      if (kProducers == 0 && more) dma_lat(kb + kBlock, st_next, ks);
     }
-    if (more)
+    if (kProducers == 0 && more)
       for (int r = wave; r < kRopeDma; r += 4) dma_rope(kb + kBlock, st_next, r);
     u32x4_t kr[2];
     if (key0 + 16 > a.rope_len) {
@@ -387,7 +417,7 @@ __global__ __launch_bounds__(256, 1) void attn_split_kernel(DecodeArgs a) {
     uint16_t* op = a.out + tok * a.o_tok;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const int cidx = threadIdx.x + 256 * j;  // 16 heads x 256 bf16 pairs
+      const int cidx = threadIdx.x + 256 * j;  // 16 heads x 256 bf16 pairs (compute waves)
       const int h = cidx >> 8, d = (cidx & 255) * 2;
       *reinterpret_cast<uint32_t*>(op + h * a.o_head + d) =
           *reinterpret_cast<const uint32_t*>(&s_o[h * kLat + d]);
@@ -609,7 +639,7 @@ extern "C" int dsk_mla_decode_attention(const dsk_bf16* q_abs, int64_t qa_tok, i
   a.o_tok = o_tok;
   a.o_head = o_head;
   hipStream_t st = as_stream(stream);
-  hipLaunchKernelGGL(attn_split_kernel, dim3(S, q_len, batch), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(attn_split_kernel, dim3(S, q_len, batch), dim3(kSplitThreads), 0, st, a);
   int rc = check_launch("attn_split_kernel");
   if (rc || S == 1) return rc;
   const dim3 mgrid(kHeads * kLat / 4 / 16, batch * q_len);
