@@ -500,6 +500,33 @@ def calibrate_copy(steps):
     print(json.dumps({"copy_bytes": COPY_BYTES, "launches": steps}), flush=True)
 
 
+def dense_gemm2(dsk, torch, reps):
+    """GEMM2's shape as one dense product (32768 x 2048 x 1408, bf16): torch's
+    library GEMM (hipBLASLt) against this build's weight-streaming kernel on the
+    fragment-tiled weight, same inputs; for timing and counter passes."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    M, N, K = 32768, 2048, 1408
+    a = torch.randn(M, K, device=dev, dtype=torch.bfloat16, generator=g)
+    w = torch.randn(N, K, device=dev, dtype=torch.bfloat16, generator=g)
+    wt = dsk.tile_weights(w[None])[0].contiguous()
+    for _ in range(10):
+        y_lib = torch.nn.functional.linear(a, w)
+        y_dsk = dsk.linear(a, wt)
+    torch.cuda.synchronize()
+    res = {"shape": [M, N, K], "max_abs_diff": (y_lib.float() - y_dsk.float()).abs().max().item()}
+    for name, f in (("hipblaslt_us", lambda: torch.nn.functional.linear(a, w)),
+                    ("dsk_linear_us", lambda: dsk.linear(a, wt))):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            f()
+        e.record()
+        torch.cuda.synchronize()
+        res[name] = s.elapsed_time(e) / reps * 1e3
+    return res
+
+
 def _pmc_per_dispatch(csv_path, kernel_substrs, counter):
     import csv
     vals = {}
@@ -560,6 +587,9 @@ def main():
                     help="only the MLA projection block and decoder layer (for profiling)")
     ap.add_argument("--mla-decode-only", action="store_true",
                     help="only the latent-cache decode attention and decode step (for profiling)")
+    ap.add_argument("--dense-gemm2", type=int, default=0, metavar="REPS",
+                    help="GEMM2's shape as a dense product: the library GEMM against "
+                         "dsk_linear_ex, REPS timed calls each")
     ap.add_argument("--ramp", action="store_true",
                     help="per-step layer times from a cold start, and a copy and a dense product "
                          "after an idle second (the clock ramp)")
@@ -582,6 +612,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.mla_only:
         print(json.dumps(bench_mla(dsk, syn, torch, HipEvents())), flush=True)
+        return
+    if args.dense_gemm2:
+        print(json.dumps(dense_gemm2(dsk, torch, args.dense_gemm2)), flush=True)
         return
     if args.mla_decode_only:
         from ds_kernels import mla as dm
