@@ -83,12 +83,14 @@ def test_rope_matches_oracle(dsk, b, s, strided):
 
 
 @pytest.mark.parametrize("d,hq,s", [(8, 3, 37), (24, 3, 37), (32, 16, 5), (48, 2, 64),
-                                    (128, 5, 9)])
+                                    (128, 5, 9), (64, 12, 33), (64, 20, 7), (16, 9, 3)])
 def test_rope_other_dims(dsk, d, hq, s):
     """Rope dims other than 64: 4 pairs per thread when d is not a multiple of 16
     (8, 24), 8 pairs otherwise; odd head counts and sequence lengths exercise the
-    multiply-shift index split. The cos/sin tables are random, not duplicated
-    halves, so the first- and second-half table reads are told apart."""
+    multiply-shift index split. A thread rotates up to 8 heads at one position, so
+    head counts of 9, 12 and 20 leave a partial last group. The cos/sin tables are
+    random, not duplicated halves, so the first- and second-half table reads are
+    told apart."""
     b = 2
     g = torch.Generator().manual_seed(d * 100 + hq + s)
     q = torch.randn(b, hq, s, d, generator=g).to(torch.bfloat16)
