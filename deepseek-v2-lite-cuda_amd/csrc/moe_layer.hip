@@ -367,7 +367,11 @@ extern "C" int dsk_moe_layer_forward_noalloc(const dsk_bf16* x, const dsk_bf16* 
     DSK_REQUIRE(eager, DSK_ERR_INVALID_ARG,
                 "moe_layer_noalloc: the first call on a device must not be under stream "
                 "capture (it resolves the device's scratch); make one eager call first");
-    DSK_REQUIRE(hipEventCreateWithFlags(&fl.done, hipEventDisableTiming) == hipSuccess,
+    // the event only tells whether the call's work has run (hipEventQuery); no
+    // timing and no system-scope fence, whose cache writeback and invalidate
+    // would cost each eager call ~2 us of GPU time
+    DSK_REQUIRE(hipEventCreateWithFlags(&fl.done, hipEventDisableTiming |
+                                                      hipEventDisableSystemFence) == hipSuccess,
                 DSK_ERR_LAUNCH, "moe_layer_noalloc: hipEventCreate failed");
   }
   void* ws = nullptr;
