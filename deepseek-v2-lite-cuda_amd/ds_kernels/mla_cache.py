@@ -39,8 +39,10 @@ class LatentKVCache:
     k_rope     [bsz, max_seq, rope_head_dim]  the RoPE key after RoPE (positions
                                               < rope_len hold it), a view
 
-    The rotated keys are valid for the cos/sin tensors that produced them: a
-    decode step given other table tensors rotates every cached key again. A
+    The rotated keys are valid for the cos/sin tables that produced them: a
+    decode step given other tables (another storage or layout, or the same
+    tensors modified in place) rotates every cached key again; views of the
+    same rows with a different position count are the same tables. A
     caller that writes kv_latent or k_pe_cache directly (not through update()
     or a decode step) must call reset_rope() (or reset()) afterwards, or the
     rotated keys of the rewritten positions stay stale.
@@ -60,7 +62,7 @@ class LatentKVCache:
         self.dtype = dtype
         self._len = 0
         self._rope_len = 0   # leading positions whose k_rope is valid
-        self._rope_tables = None   # identity of the cos/sin tables that rotated them
+        self._rope_tables = None   # (identity, cos, sin) of the tables that rotated them
         w = kv_lora_rank + rope_head_dim
         self.rows = torch.zeros((bsz, max_seq, w + rope_head_dim), dtype=dtype,
                                 device=self.device)
@@ -144,12 +146,19 @@ class LatentKVCache:
 
     def use_rope_tables(self, cos: torch.Tensor, sin: torch.Tensor) -> None:
         """Called by a decode step with its tables: rotated keys made with other
-        tables (another tensor, or these modified in place) are dropped."""
-        key = (cos.data_ptr(), sin.data_ptr(), tuple(cos.shape), tuple(sin.shape), cos.dtype,
-               sin.dtype, cos._version, sin._version)
-        if key != self._rope_tables:
+        tables (another storage, other strides, or these modified in place) are
+        dropped. The cache holds the tables it last saw, so their memory cannot be
+        handed to another tensor while their address identifies them; a view of
+        the same rows with another length (cos[:seq_len] as the reference passes
+        it, growing every step) is the same table, and keeps the rotated keys."""
+        def ident(t):
+            # everything but the position count: batch dims, row width, layout
+            return (t.data_ptr(), t.stride(), tuple(t.shape[:-2]), t.shape[-1], t.dtype,
+                    t._version)
+        key = (ident(cos), ident(sin))
+        if self._rope_tables is None or key != self._rope_tables[0]:
             self._rope_len = 0
-            self._rope_tables = key
+        self._rope_tables = (key, cos, sin)
 
     def __repr__(self) -> str:
         used = (self._len * (self.kv_lora_rank + self.rope_head_dim) * self.rows.element_size()

@@ -173,3 +173,35 @@ def test_rope_tables_identity_and_reset_rope():
     c.k_pe_cache[:, :2] = 1.0            # direct write into the raw keys
     c.reset_rope()
     assert c.rope_len == 0 and c.current_len == 4
+
+
+def test_rope_tables_growing_views_and_recycled_memory():
+    """Views of one table with a growing position count (cos[:seq_len], as the
+    reference's rotary embedding returns them each step) keep the rotated keys;
+    a table freed and replaced by new values cannot alias the old one, because
+    the cache holds the tables it used."""
+    c = LatentKVCache(1, 8, kv_lora_rank=16, rope_head_dim=8, device="cpu")
+    c.update(torch.zeros(1, 4, 16), torch.zeros(1, 4, 8))
+    cos_full, sin_full = torch.rand(16, 8), torch.rand(16, 8)
+    c.use_rope_tables(cos_full[:4], sin_full[:4])
+    c._rope_len = 4
+    c.use_rope_tables(cos_full[:5], sin_full[:5])   # same rows, one more position
+    assert c.rope_len == 4
+    c.use_rope_tables(cos_full[1:6], sin_full[1:6])  # shifted rows: other positions
+    assert c.rope_len == 0
+    # per-sequence tables [b, s, d]: the batch dims count, the length does not
+    cb = torch.rand(2, 16, 8)
+    c.use_rope_tables(cb[:, :4], cb[:, :4])
+    c._rope_len = 4
+    c.use_rope_tables(cb[:, :6], cb[:, :6])
+    assert c.rope_len == 4
+    c.use_rope_tables(cb[:1, :6], cb[:1, :6])
+    assert c.rope_len == 0
+    # the tables in use stay alive: a new tensor never takes their address
+    c._rope_len = 4
+    held = c._rope_tables[1].data_ptr()
+    del cb
+    fresh = [torch.rand(1, 6, 8) for _ in range(8)]
+    assert all(t.data_ptr() != held for t in fresh)
+    c.use_rope_tables(fresh[0], fresh[0])
+    assert c.rope_len == 0
