@@ -42,6 +42,24 @@ def test_rms_norm_f32(dsk, rows, H):
     np.testing.assert_allclose(np32(out), ref, rtol=F32_TOL, atol=1e-6)
 
 
+@pytest.mark.parametrize("scale", [1.0, 1e4, 1e-4])
+def test_rms_norm_3d_input_and_magnitudes(dsk, scale):
+    """[bsz, seq, hidden] input (the reference test's 3-D case, flattened rows),
+    at ordinary, large and small magnitudes (the normalised output has the same
+    scale whatever the input's), plus an all-zero row (eps keeps it finite: 0)."""
+    g = torch.Generator().manual_seed(31)
+    x = (torch.randn(2, 32, 512, generator=g) * scale).to(torch.bfloat16)
+    x[1, 5] = 0
+    w = torch.rand(512, generator=g) + 0.5
+    out = dsk.rms_norm(x.to(DEV), w.to(DEV), 1e-6)
+    assert out.shape == (2, 32, 512) and out.dtype == torch.bfloat16
+    o = np32(out)
+    assert np.isfinite(o).all()
+    assert (o[1, 5] == 0).all()
+    ref = ol.rms_norm(np32(x).reshape(-1, 512), w.numpy(), 1e-6).reshape(2, 32, 512)
+    assert max_rel_err(o, ref) <= BF16_TOL
+
+
 def test_rms_norm_strided_latent_view(dsk):
     """Normalise the 512-wide latent inside the 576-wide kv_a output in place."""
     g = torch.Generator().manual_seed(3)
@@ -112,6 +130,20 @@ def test_kv_upproj(dsk, rows):
     ref = om.grouped_linear(np32(n), np32(w)[None], np.array([0, rows], np.int32))
     assert out.shape == (rows, 4096)
     assert max_rel_err(np32(out), ref) <= BF16_TOL
+
+
+def test_kv_upproj_3d_input(dsk):
+    """[bsz, seq, 512] in, [bsz, seq, 4096] out (the reference test's 3-D case),
+    the same rows as the 2-D call bit for bit, and against fp32 products."""
+    g = torch.Generator().manual_seed(5)
+    n = (torch.randn(2, 32, 512, generator=g) * 0.1).to(torch.bfloat16)
+    w = (torch.randn(4096, 512, generator=g) * 0.02).to(torch.bfloat16)
+    out = dsk.kv_upproj(n.to(DEV), w.to(DEV))
+    assert out.shape == (2, 32, 4096)
+    flat = dsk.kv_upproj(n.reshape(64, 512).to(DEV), w.to(DEV))
+    assert torch.equal(out.reshape(64, 4096), flat)
+    ref = np32(n).reshape(64, 512) @ np32(w).T
+    assert max_rel_err(np32(out).reshape(64, 4096), ref) <= BF16_TOL
 
 
 @pytest.mark.parametrize("M,K,N", [(8, 2048, 3072), (130, 2048, 576), (1000, 512, 4096),
@@ -418,6 +450,29 @@ def test_decoder_layer_matches_oracle(mla_setup):
     ref = ol.decoder_layer(np32(x), p)
     assert out.shape == (b, s, 2048)
     assert max_rel_err(np32(out), ref) <= BF16_TOL
+
+
+def test_decoder_layer_causality(mla_setup):
+    """Causality of the layer (the property the reference checks on its module,
+    test_reference_decoder_layer.py:80): changing the tokens from position p on
+    leaves every output before p bit for bit as it was. The attention masks the
+    later keys to exact zeros, and every MoE row is computed from its own token
+    in a fixed order, whichever rows share its groups."""
+    dm, w, W, wn = mla_setup
+    from ds_kernels import synthetic as syn
+    P = dm.DecoderLayerWeights.from_tensors(w, syn.moe_weights(), torch.device(DEV))
+    b, s, p = 2, 96, 40
+    g = torch.Generator().manual_seed(17)
+    x = torch.randn(b, s, 2048, generator=g).to(torch.bfloat16)
+    x2 = x.clone()
+    x2[:, p:] = torch.randn(b, s - p, 2048, generator=g).to(torch.bfloat16)
+    cos, sin = dm.yarn_cos_sin(s)
+    cos, sin = cos.to(DEV), sin.to(DEV)
+    out = dm.decoder_layer_forward(x.to(DEV), P, cos, sin)
+    out2 = dm.decoder_layer_forward(x2.to(DEV), P, cos, sin)
+    torch.cuda.synchronize()
+    assert torch.equal(out[:, :p], out2[:, :p])
+    assert not torch.equal(out[:, p:], out2[:, p:])
 
 
 def test_decoder_layer_matches_oracle_large_groups(mla_setup):
