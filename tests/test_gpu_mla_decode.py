@@ -209,6 +209,53 @@ def test_decode_attention_op_rotated_keys(setup):
     assert torch.equal(out.transpose(0, 1).cpu(), a.cpu()) and torch.equal(c.cpu(), a.cpu())
 
 
+@pytest.mark.parametrize("b,n", [(1, 1), (4, 1), (8, 1), (16, 1), (1, 8), (2, 4)])
+def test_decode_attention_op_split_plans(setup, b, n):
+    """The op over a 4096-token cache at the batch shapes whose key-split plans
+    differ (64 splits of one 64-key block at b = 1, 32 of two at b = 4 and 8 and
+    for 8 new tokens, 16 of four at b = 16) against an fp32 torch restatement of
+    absorbed attention (RMS-scaled latents, rotated keys, causal over the new
+    tokens), and one sequence of the batch against the same sequence alone,
+    which runs under the one-sequence plan."""
+    dsk, W, A, wn, _, _ = setup
+    from ds_kernels import mla as dm
+    L = 4096
+    cos, sin = dm.yarn_cos_sin(L)
+    cos, sin = cos.to(torch.bfloat16).to(DEV), sin.to(torch.bfloat16).to(DEV)
+    g = torch.Generator().manual_seed(100 * b + n)
+    raw = torch.randn(b, L, 576, generator=g).to(torch.bfloat16).to(DEV)
+    q_abs = (torch.randn(b * n, 16, 512, generator=g) * 0.1).to(torch.bfloat16).to(DEV)
+    q_pe = torch.randn(b * n, 16, 64, generator=g).to(torch.bfloat16).to(DEV)
+    rows = _rotated_rows(dsk, raw, cos, sin)
+    scale = W.softmax_scale
+    got = dsk.mla_decode_attention(q_abs, q_pe, rows[..., :512], rows[..., 512:576], cos, sin,
+                                   scale, k_rope=rows[..., 576:640], rope_len=L)
+    # fp32 reference: the query rotated at its position L - n + j as the keys are
+    from ds_kernels import ops
+    c = cos[L - n:L][None, None].expand(b, 1, n, 64)
+    s = sin[L - n:L][None, None].expand(b, 1, n, 64)
+    q_rot = ops.rope_single(q_pe.view(b, n, 16, 64).permute(0, 2, 1, 3), c, s)
+    q_rot = q_rot.permute(0, 2, 1, 3).reshape(b, n * 16, 64).float()
+    x = rows[..., :512].float()
+    xn = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6)
+    kr = rows[..., 576:640].float()
+    sc = (torch.matmul(q_abs.view(b, n * 16, 512).float(), xn.transpose(1, 2).contiguous())
+          + torch.matmul(q_rot, kr.transpose(1, 2).contiguous())) * scale
+    pos = (L - n + torch.arange(n, device=DEV)).repeat_interleave(16)     # [n * 16]
+    sc = sc.masked_fill(torch.arange(L, device=DEV)[None, None, :] > pos[None, :, None],
+                        float("-inf"))
+    ref = torch.matmul(torch.softmax(sc, -1), xn).view(b * n, 16, 512)
+    torch.cuda.synchronize()
+    assert max_rel_err(np32(got), np32(ref)) <= BF16_TOL
+    i = b - 1
+    alone = dsk.mla_decode_attention(q_abs[i * n:(i + 1) * n], q_pe[i * n:(i + 1) * n],
+                                     rows[i:i + 1, :, :512], rows[i:i + 1, :, 512:576], cos, sin,
+                                     scale, k_rope=rows[i:i + 1, :, 576:640], rope_len=L)
+    torch.cuda.synchronize()
+    assert max_rel_err(np32(alone), np32(ref[i * n:(i + 1) * n])) <= BF16_TOL
+    assert max_rel_err(np32(alone), np32(got[i * n:(i + 1) * n])) <= 1e-2
+
+
 def test_decode_after_reference_update(setup):
     """A cache filled through the reference API (update() with raw rows, nothing
     rotated) and then a decode step: the kernel rotates the whole prefix, and the
