@@ -524,18 +524,18 @@ namespace {
 // Key splits per query token: enough workgroups to give every CU one
 // (DSK_DECODE_WGS; the split kernel's LDS ring admits one workgroup per CU), at
 // most kMaxSplits, at least one 64-key block each. Each split writes a 32 KB
-// partial that the merge reads back, against 74 KB of cache per block, so two
-// blocks per split are taken wherever that still leaves half the CUs busy: at
-// L = 4096, b = 4 runs 13.6 us on 32 splits of two blocks against 15.1 us on 64
-// of one, while b = 1 keeps its 64 single-block splits (9.9 us against 11.2).
+// partial that the merge reads back, against 74 KB of cache per block, so a
+// plan of one block per split takes two wherever that still leaves half the CUs
+// busy: at L = 4096, b = 4 runs 13.6 us on 32 splits of two blocks against
+// 15.1 us on 64 of one, while b = 1 keeps its 64 single-block splits (9.9 us
+// against 11.2).
 void split_plan(int batch, int q_len, int kv_len, int* n_splits, int* split_blocks) {
   const int blocks = (kv_len + kBlock - 1) / kBlock;
   const int64_t tokens = (int64_t)batch * q_len;
   int want = (int)std::min<int64_t>(blocks, std::max<int64_t>(1, (DSK_DECODE_WGS + tokens - 1) / tokens));
   want = std::min(want, kMaxSplits);
-  const int halved = std::min(want, blocks / 2);
-  if (halved >= 1 && tokens * halved >= DSK_DECODE_WGS / 2) want = halved;
   int per = (blocks + want - 1) / want;
+  if (per == 1 && blocks >= 2 && tokens * ((blocks + 1) / 2) >= DSK_DECODE_WGS / 2) per = 2;
   *split_blocks = per;
   *n_splits = (blocks + per - 1) / per;
 }

@@ -206,6 +206,28 @@ def test_attn_pack_ex_validation(dsk):
     assert call(cs_bs=-64) == 1 and "stride" in _err(dsk)
 
 
+def test_mla_decode_split_plan(dsk):
+    """Key splits per query token, read back from the workspace size (a 32 KB
+    partial and 128 B of running max and sum per split and token): about 256
+    workgroups; a plan of one 64-key block per split takes two where that
+    leaves 128 or more workgroups; plans of several blocks are left alone."""
+    per_split = (16 * 512 + 32) * 4
+
+    def splits(b, n, L):
+        ws = dsk.lib.dsk_mla_decode_workspace_size(b, n, L)
+        return ws // (b * n * per_split)
+    assert splits(1, 1, 4096) == 64     # one block each: only 64 workgroups
+    assert splits(3, 1, 4096) == 64     # two blocks would leave 96 workgroups
+    assert splits(4, 1, 4096) == 32     # two blocks each: 128 workgroups
+    assert splits(8, 1, 4096) == 32
+    assert splits(16, 1, 4096) == 16    # four blocks each
+    assert splits(1, 8, 4096) == 32
+    assert splits(2, 4, 4096) == 32
+    assert splits(8, 1, 2100) == 17     # 33 blocks: two per split, not three
+    assert splits(4, 1, 2100) == 33     # two per split would leave 68 workgroups
+    assert splits(64, 1, 4096) == 4
+
+
 def test_mla_decode_validation(dsk):
     lib = dsk.lib
     ws = lib.dsk_mla_decode_workspace_size(1, 1, 4096)
