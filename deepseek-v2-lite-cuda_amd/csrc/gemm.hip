@@ -1069,13 +1069,18 @@ __device__ __forceinline__ void skinny_route_prologue(const GemmArgs& p,
   __syncthreads();
 }
 
-// NB: 32-row weight blocks per workgroup (SwiGLU: the gate and the up block);
+// NB: 32-row weight blocks per workgroup (SwiGLU with NB = 2: a gate and an up
+// block of 32 output columns; SwiGLU with NB = 1: one block whose rows 0-15 are
+// the gate rows and 16-31 the up rows of 16 output columns);
 // NW: waves per workgroup, each one slice of K.
 // The kernel body, on workgroup `bid` of the small-group grid (a device function
 // so that other launches can host the same work in extra workgroups).
 template <int MT, bool SWIGLU, bool GATHER, bool TILED, int NB = 2, int NW = kSkinnyWaves>
 __device__ __forceinline__ void skinny_gemm_body(const GemmArgs& p, int n_blocks, int bid) {
-  static_assert(NB == 2 || (!SWIGLU && NB == 1), "SwiGLU pairs a gate and an up block");
+  static_assert(NB == 2 || NB == 1, "one or two 32-row weight blocks");
+  // SwiGLU in 16-column units: gate row r and up row r + 16 of the block meet in
+  // one lane (accumulator i holds block row 8 (i / 4) + 4 h + i % 4)
+  constexpr bool kHalfUnit = SWIGLU && NB == 1;
   static_assert(NW == 4 || NW == 8, "reduction written for 4 or 8 waves");
   // partial sums of the upper half of the waves (8 waves), then of waves 1..3
   __shared__ floatx4_t red[NW == 8 ? 4 : 3][NB][MT][4][64];
@@ -1156,7 +1161,14 @@ __device__ __forceinline__ void skinny_gemm_body(const GemmArgs& p, int n_blocks
   uint32_t woff[NB];
 #pragma unroll
   for (int blk = 0; blk < NB; ++blk) {
-    if constexpr (TILED) {
+    if constexpr (TILED && kHalfUnit) {
+      // 16 gate rows from one half of a 32-row fragment, 16 up rows from the
+      // same half of the matching up fragment (N % 32 == 0 for tiled weights)
+      const int u = min(nb, p.N / 16 - 1);
+      const int rb = (r32 < 16 ? 0 : p.up_row_offset / 32) + u / 2;
+      const int src = (u & 1) * 16 + (r32 & 15) + 32 * h;  // lane of that row in the fragment
+      woff[blk] = (uint32_t)((((int64_t)rb * (p.K / 16) + k_beg / 16) * 512 + src * 8) * 2);
+    } else if constexpr (TILED) {
       int rb;
       if constexpr (SWIGLU) {
         const int cb = min(nb, p.N / 32 - 1);
@@ -1167,7 +1179,10 @@ __device__ __forceinline__ void skinny_gemm_body(const GemmArgs& p, int n_blocks
       woff[blk] = (uint32_t)((((int64_t)rb * (p.K / 16) + k_beg / 16) * 512 + lane * 8) * 2);
     } else {
       int row;
-      if constexpr (SWIGLU) {
+      if constexpr (kHalfUnit) {
+        const int col = min(nb * 16 + (r32 & 15), p.N - 1);
+        row = r32 < 16 ? col : p.up_row_offset + col;
+      } else if constexpr (SWIGLU) {
         const int col = min(nb * 32 + r32, p.N - 1);
         row = blk == 0 ? col : p.up_row_offset + col;
       } else {
@@ -1317,14 +1332,19 @@ __device__ __forceinline__ void skinny_gemm_body(const GemmArgs& p, int n_blocks
         const int m = m0 + mt * 32 + r32;
         uint16_t* crow = second ? p.C2 + (int64_t)m * p.ldc2 : Cg + (int64_t)m * p.ldc;
         constexpr int JN = SWIGLU ? 1 : NB;
+        constexpr int QG = kHalfUnit ? 2 : 4;  // half units: groups 0-1 gate, 2-3 up
 #pragma unroll
         for (int j = 0; j < JN; ++j) {
 #pragma unroll
-          for (int qg = 0; qg < 4; ++qg) {
-            const int nbase = SWIGLU ? nb * 32 : nb * 32 * NB + j * 32;
+          for (int qg = 0; qg < QG; ++qg) {
+            const int nbase = kHalfUnit ? nb * 16 : SWIGLU ? nb * 32 : nb * 32 * NB + j * 32;
             const int n = nbase + 8 * qg + 4 * h;
             float v[4];
-            if constexpr (SWIGLU) {
+            if constexpr (kHalfUnit) {
+              const floatx4_t gt = total(0, mt, qg), up = total(0, mt, qg + 2);
+#pragma unroll
+              for (int c = 0; c < 4; ++c) v[c] = silu_f(gt[c]) * up[c];
+            } else if constexpr (SWIGLU) {
               const floatx4_t gt = total(0, mt, qg), up = total(1, mt, qg);
 #pragma unroll
               for (int c = 0; c < 4; ++c) v[c] = silu_f(gt[c]) * up[c];
@@ -1459,6 +1479,21 @@ static int launch_skinny_gemm(const GemmArgs& a, hipStream_t st) {
       const int n_blocks = (a.N + 31) / 32;
       hipLaunchKernelGGL((skinny_gemm_kernel<MT, SWIGLU, GATHER, TILED, 1, 8>),
                          dim3((unsigned)(GL * n_blocks)), dim3(64 * 8), 0, st, a, n_blocks);
+      return check_launch("skinny_gemm_kernel");
+    }
+  }
+  if constexpr (SWIGLU) {
+    // Fewer than two 32-column workgroups per CU (a one-token step: 8 groups x
+    // 44): a CU's fetch rate bounds each workgroup's weight stream, so the CUs
+    // that hold two set the launch time. 16-column units halve the bytes per
+    // workgroup and spread them over the CUs more evenly. Measured on MI355X:
+    // GEMM1 at T = 1 27.7 -> 25.2 us (bitwise the same output); at T = 2-4 (704
+    // or more workgroups) unchanged, at T = 16 1.4 us and at T = 64 11 us slower.
+    if (GL * ((a.N + 31) / 32) < 2 * (int64_t)num_cus()) {
+      const int n_blocks = (a.N + 15) / 16;
+      hipLaunchKernelGGL((skinny_gemm_kernel<MT, true, GATHER, TILED, 1, kSkinnyWaves>),
+                         dim3((unsigned)(GL * n_blocks)), dim3(kSkinnyThreads), 0, st, a,
+                         n_blocks);
       return check_launch("skinny_gemm_kernel");
     }
   }

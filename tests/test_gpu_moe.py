@@ -242,6 +242,25 @@ def test_gemm_small_groups(dsk, counts):
     assert max_rel_err(np32(out2), om.grouped_linear(np32(h), np32(w2), off)) <= BF16_TOL
 
 
+@pytest.mark.parametrize("I", [1400, 100])
+def test_gemm1_swiglu_few_groups_ragged_width(dsk, I):
+    """Few busy groups (the grid of a one-token step) run SwiGLU in 16-column
+    units; with an intermediate size that is not a multiple of 16 the last unit
+    reads clamped weight rows and writes only the columns below I."""
+    counts = [1, 0, 3, 2]
+    E = len(counts)
+    off = om.scan(np.array(counts, np.int32))
+    S = int(off[-1])
+    offd = torch.from_numpy(off).to(DEV)
+    a, w = _gemm_inputs(S, 2 * I, 2048, E, 500 + I)
+    ref = om.swiglu(om.grouped_linear(np32(a), np32(w), off))
+    out = dsk.moe_gemm1_swiglu(a.to(DEV), w.to(DEV), offd)
+    assert out.shape == (S, I)
+    assert max_rel_err(np32(out), ref) <= BF16_TOL
+    unfused = dsk.swiglu(dsk.moe_gemm1(a.to(DEV), w.to(DEV), offd))
+    assert max_rel_err(np32(unfused), ref) <= BF16_TOL
+
+
 def test_gemm_small_groups_caller_offsets_not_sorted(dsk):
     """Offsets from a caller need not increase: here busy groups (3) outnumber
     the rows (2), group 4 alone covers row 1, and groups 0, 2 and 4 (identical
