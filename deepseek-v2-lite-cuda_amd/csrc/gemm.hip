@@ -259,8 +259,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void grouped_gemm_kernel
     const int mb = s_mb[lo], gme = s_me[lo];
     const int mt = (gme - mb + BM - 1) / BM;
     const int nblk = (gme - mb + 31) / 32;
-    const int nt = local / mt;
-    const int mi = local - nt * mt;
+    int nt, mi;
+    sched_group_tile(local, mt, NT, &nt, &mi);
     const int m0 = mb + 32 * (mi * nblk / mt);
     const int me = min(mb + 32 * ((mi + 1) * nblk / mt), gme);
     return Tile{lo, m0, me, nt * OUT_N};
@@ -649,8 +649,8 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void wide_gemm_kernel(GemmArgs 
     const int mb = s_mb[lo], gme = s_me[lo];
     const int mt = (gme - mb + kWideBM - 1) / kWideBM;
     const int nblk = (gme - mb + 31) / 32;
-    const int nt = local / mt;
-    const int mi = local - nt * mt;
+    int nt, mi;
+    sched_group_tile(local, mt, NT, &nt, &mi);
     const int m0 = mb + 32 * (mi * nblk / mt);
     const int me = min(mb + 32 * ((mi + 1) * nblk / mt), gme);
     return Tile{lo, m0, me, nt * OUT_N};

@@ -46,6 +46,29 @@ DSK_HD int sched_tile_index(int xcd, int slot, int t, int per_xcd) {
   return ((q / kTileChunk) * kXcds + xcd) * kTileChunk + q % kTileChunk;
 }
 
+// Order of a group's tiles (mt M tiles x nt_count N tiles): N-major inside
+// panels of kPanelM M tiles, so that a chunk of 16 consecutive tiles of a large
+// group (the shared experts' 16 M tiles at T = 4096) covers 8 M tiles x 2 N
+// tiles instead of 16 M tiles x 1 N tile, and fewer XCDs re-read each token
+// row; groups of at most kPanelM M tiles (the routed experts) are one panel,
+// all M tiles of an N tile side by side, sharing its weights. Measured on
+// MI355X at T = 4096: GEMM1 reads 1.165 GB past the L2 per launch against
+// 1.238 GB with one panel per group and 1.229 GB with panels of 16, in the same
+// time (365.6 against 366.0 us; bitwise the same output).
+constexpr int kPanelM = 8;
+DSK_HD void sched_group_tile(int local, int mt, int nt_count, int* nt, int* mi) {
+  if (mt <= kPanelM) {
+    *nt = local / mt;
+    *mi = local - *nt * mt;
+    return;
+  }
+  const int p = local / (kPanelM * nt_count);
+  const int r = local - p * kPanelM * nt_count;
+  const int ps = mt - p * kPanelM < kPanelM ? mt - p * kPanelM : kPanelM;  // last panel may be short
+  *nt = r / ps;
+  *mi = p * kPanelM + (r - *nt * ps);
+}
+
 // The largest number of tiles any workgroup runs (nwg a multiple of 8).
 DSK_HD int sched_max_tiles(int total, int nwg) {
   int m = 0;

@@ -6,6 +6,8 @@
 //   2. The launcher's grid keeps every workgroup within the LDS row table,
 //      for any row table size, group sizes, M and CU count, at the kernel's
 //      real tile count (which the launcher bounds from above).
+//   3. A group's tile order (panels of M tiles) maps its local tile indices
+//      onto its (N tile, M tile) pairs one to one.
 #include <cstdio>
 #include <cstdlib>
 #include <algorithm>
@@ -71,6 +73,18 @@ int main() {
           return fail("workgroup beyond the row table", total, nwg, rt);
         if (sched_max_tiles((int)upper, (int)nwg) > rt)
           return fail("bound beyond the row table", upper, nwg, rt);
+      }
+    }
+  }
+  // 3. the panel order inside a group is a bijection
+  for (int mt = 1; mt <= 4 * kPanelM + 3; ++mt) {
+    for (int nc = 1; nc <= 24; ++nc) {
+      seen.assign(mt * nc, 0);
+      for (int l = 0; l < mt * nc; ++l) {
+        int nt = -1, mi = -1;
+        sched_group_tile(l, mt, nc, &nt, &mi);
+        if (nt < 0 || nt >= nc || mi < 0 || mi >= mt) return fail("group tile out of range", mt, nc, l);
+        if (seen[mi * nc + nt]++) return fail("group tile run twice", mt, nc, l);
       }
     }
   }

@@ -1,7 +1,8 @@
 """CPU check of the grouped GEMM kernels' persistent-grid tile schedule
 (csrc/gemm_sched.hpp, shared by the kernels and their launchers): every tile is
-run exactly once, and the launchers' grid keeps each workgroup within the LDS
-row table of the gathered kernels (which compute nothing past it). The C++
+run exactly once, the launchers' grid keeps each workgroup within the LDS row
+table of the gathered kernels (which compute nothing past it), and the panel
+order of a group's tiles is a bijection. The C++
 check is built with g++ from tests/gemm_schedule_check.cpp."""
 import os
 import shutil
