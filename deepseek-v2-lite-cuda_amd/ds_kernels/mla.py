@@ -8,7 +8,7 @@ layout) for q_proj, kv_a_proj_with_mqa and o_proj, `rms_norm` straight on the
 `kv_upproj`, `rope` on strided q_pe / k_pe views with the position tables
 broadcast over the batch (no materialised copies), and the fused MoE layer
 (`moe_layer_forward`). In the causal attention core the two batched products
-stay torch, as the survey scopes it; the scale, causal mask, fp32 softmax and
+stay torch (the attention core is outside the kernel scope); the scale, causal mask, fp32 softmax and
 bf16 rounding between them are one pass of `attn_softmax_`, at the reference's
 precision.
 """
