@@ -24,6 +24,9 @@ struct GemmArgs {
                            // (0: unknown, M is used); selects the small-group kernel
   int offsets_sorted;      // offsets never decrease (the fused layer's own): the small-
                            // group grid then launches min(G, M) group ordinals, else G
+  int chunk_m_tiles;       // large-group kernels: M tiles of a typical group, so that
+                           // tiles are dealt to the XCDs a group at a time (0: chunks
+                           // of kTileChunk tiles; gemm_sched.hpp sched_chunk)
   int64_t a_group_stride;  // skinny kernel: elements between the A bases of consecutive
   int64_t c_group_stride;  // groups, and of the C bases (0: one base, rows by offsets)
   int b_tiled;             // B stored as MFMA fragments (see the fragment-tiled layout in

@@ -240,7 +240,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void grouped_gemm_kernel
   const int xcd = blockIdx.x & 7;
   const int slot = blockIdx.x >> 3;
   const int per_xcd = gridDim.x >> 3;
-  const int ntiles = sched_slot_tiles(sched_xcd_tiles(total_tiles, xcd), slot, per_xcd);
+  const int chunk = sched_chunk(p.chunk_m_tiles, NT);
+  const int ntiles = sched_slot_tiles(sched_xcd_tiles(total_tiles, xcd, chunk), slot, per_xcd);
   if (ntiles == 0) return;  // uniform: no work for this workgroup
   const int nk = p.K / BK;
   const int total = ntiles * nk;  // stages in this workgroup's stream
@@ -249,7 +250,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N, 1) void grouped_gemm_kernel
     int g, m0, me, n0;  // rows [m0, me) of group g, output columns from n0
   };
   auto decode = [&](int t) -> Tile {
-    const int W = sched_tile_index(xcd, slot, t, per_xcd);
+    const int W = sched_tile_index(xcd, slot, t, per_xcd, chunk);
     int lo = 0, hi = G - 1;
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
@@ -630,7 +631,8 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void wide_gemm_kernel(GemmArgs 
   const int xcd = blockIdx.x & 7;
   const int slot = blockIdx.x >> 3;
   const int per_xcd = gridDim.x >> 3;
-  const int ntiles = sched_slot_tiles(sched_xcd_tiles(total_tiles, xcd), slot, per_xcd);
+  const int chunk = sched_chunk(p.chunk_m_tiles, NT);
+  const int ntiles = sched_slot_tiles(sched_xcd_tiles(total_tiles, xcd, chunk), slot, per_xcd);
   if (ntiles == 0) return;
   const int nk = p.K / kWideBK;  // even (K % 128 == 0, checked by the launcher)
   const int total = ntiles * nk;
@@ -639,7 +641,7 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void wide_gemm_kernel(GemmArgs 
     int g, m0, me, n0;
   };
   auto decode = [&](int t) -> Tile {
-    const int W = sched_tile_index(xcd, slot, t, per_xcd);
+    const int W = sched_tile_index(xcd, slot, t, per_xcd, chunk);
     int lo = 0, hi = G - 1;
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
@@ -1437,10 +1439,12 @@ static int launch_grouped_gemm(const GemmArgs& a, hipStream_t st) {
   const int64_t nt = (a.N + Cfg::OUT_N - 1) / Cfg::OUT_N;
   // upper bound on the kernel's tile count (a group of n rows has ceil(n/BM) M tiles)
   const int64_t upper = ((int64_t)(a.M + BM - 1) / BM + (a.offsets ? G : 0)) * nt;
-  const int64_t nwg = sched_workgroups(upper, num_cus(), GATHER ? Cfg::ROW_TILES : 0);
+  const int chunk = sched_chunk(a.chunk_m_tiles, (int)nt);
+  const int64_t nwg = sched_workgroups(upper, num_cus(), GATHER ? Cfg::ROW_TILES : 0, chunk);
   // the gathered kernel stages every tile's row indices in an LDS table of
   // ROW_TILES tiles and computes nothing if its share is larger
-  if (GATHER && (upper > INT32_MAX || sched_max_tiles((int)upper, (int)nwg) > Cfg::ROW_TILES))
+  if (GATHER &&
+      (upper > INT32_MAX || sched_max_tiles((int)upper, (int)nwg, chunk) > Cfg::ROW_TILES))
     return fail(DSK_ERR_INVALID_ARG, "grouped_gemm: a workgroup's tiles exceed the LDS row table");
   hipLaunchKernelGGL(kern, dim3((unsigned)nwg), dim3(Cfg::THREADS), Cfg::LDS_BYTES, st, a);
   return check_launch("grouped_gemm_kernel");
@@ -1455,8 +1459,10 @@ static int launch_wide_gemm(const GemmArgs& a, hipStream_t st) {
   const int G = a.offsets != nullptr ? a.G : 1;
   const int64_t nt = (a.N + OUT_N - 1) / OUT_N;
   const int64_t upper = ((int64_t)(a.M + kWideBM - 1) / kWideBM + (a.offsets ? G : 0)) * nt;
-  const int64_t nwg = sched_workgroups(upper, num_cus(), GATHER ? kWideRowTiles : 0);
-  if (GATHER && (upper > INT32_MAX || sched_max_tiles((int)upper, (int)nwg) > kWideRowTiles))
+  const int chunk = sched_chunk(a.chunk_m_tiles, (int)nt);
+  const int64_t nwg = sched_workgroups(upper, num_cus(), GATHER ? kWideRowTiles : 0, chunk);
+  if (GATHER &&
+      (upper > INT32_MAX || sched_max_tiles((int)upper, (int)nwg, chunk) > kWideRowTiles))
     return fail(DSK_ERR_INVALID_ARG, "wide_gemm: a workgroup's tiles exceed the LDS row table");
   hipLaunchKernelGGL(kern, dim3((unsigned)nwg), dim3(64 * kWideWaves), kWideLdsBytes, st, a);
   return check_launch("wide_gemm_kernel");

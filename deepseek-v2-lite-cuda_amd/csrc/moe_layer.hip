@@ -17,6 +17,7 @@
 #include "dsk_internal.hpp"
 #include "route_token.hpp"
 
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 
@@ -49,6 +50,24 @@ static FusedLayout fused_layout(int T, int E, int K, int nsh, int H, int I) {
   L.y = take(Stot * H * 2);
   L.total = off;
   return L;
+}
+
+#ifndef DSK_GROUP_CHUNKS
+#define DSK_GROUP_CHUNKS 1
+#endif
+// M tiles (of 256 rows) of a typical routed group, for dealing the large-group
+// GEMMs' tiles to the XCDs one routed group at a time (GemmArgs::chunk_m_tiles),
+// or 0 (chunks of the default size) where that deal would not be even: the E
+// routed groups make E chunks and the always-on groups (T rows each) must fill
+// whole chunks, the count of all chunks a multiple of the 8 XCDs. At T = 4096
+// (E = 64, K = 6, 2 always-on groups): 2 M tiles, 64 + 16 chunks.
+static int group_chunk_m_tiles(int T, int E, int K, int nsh) {
+  if (!DSK_GROUP_CHUNKS || E % 8 != 0) return 0;
+  const int64_t avg_rows = ((int64_t)T * K + E - 1) / E;
+  const int mt = (int)std::max<int64_t>(1, (avg_rows + 255) / 256);
+  const int64_t always_on = (int64_t)nsh * ((T + 255) / 256);  // their M tiles
+  if (always_on % mt != 0 || (always_on / mt) % 8 != 0) return 0;
+  return mt;
 }
 
 // Everything after the gate: route -> permutation -> GEMM1+SwiGLU -> GEMM2 ->
@@ -120,6 +139,7 @@ static int layer_after_gate(const float* logits, int n_parts, int64_t part_strid
   g1.up_row_offset = I;
   g1.max_group_rows = T;  // a token routes to an expert at most once; shared groups hold T
   g1.b_tiled = weight_layout == DSK_LAYOUT_TILED;
+  g1.chunk_m_tiles = group_chunk_m_tiles(T, E, K, nsh);
   if (route_in_gemm) {
     g1.rt_parts = logits;
     g1.rt_n_parts = n_parts;
@@ -148,6 +168,7 @@ static int layer_after_gate(const float* logits, int n_parts, int64_t part_strid
   g2.offsets_sorted = 1;
   g2.max_group_rows = T;
   g2.b_tiled = weight_layout == DSK_LAYOUT_TILED;
+  g2.chunk_m_tiles = g1.chunk_m_tiles;
   if ((rc = run_gemm(g2, false, st))) return rc;
   if ((rc = mark(3))) return rc;
 

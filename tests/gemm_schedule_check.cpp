@@ -2,7 +2,7 @@
 // the host compiler alone by tests/test_gemm_schedule.py. Prints "OK" or the
 // first failing case and exits non-zero.
 //   1. Every tile of a launch is run by exactly one workgroup, whatever the
-//      tile count and grid size.
+//      tile count, grid size and chunk size.
 //   2. The launcher's grid keeps every workgroup within the LDS row table,
 //      for any row table size, group sizes, M and CU count, at the kernel's
 //      real tile count (which the launcher bounds from above).
@@ -26,23 +26,25 @@ static int fail(const char* what, long long a, long long b, long long c) {
 int main() {
   // 1. coverage: each tile exactly once
   std::vector<int> seen;
-  for (int nwg = 8; nwg <= 512; nwg += 8) {
-    for (int total = 0; total <= 3000; total += (total < 300 ? 1 : 37)) {
-      seen.assign(total, 0);
-      long long sum = 0;
-      for (int x = 0; x < kXcds; ++x) {
-        const int xt = sched_xcd_tiles(total, x);
-        for (int slot = 0; slot < nwg / kXcds; ++slot) {
-          const int n = sched_slot_tiles(xt, slot, nwg / kXcds);
-          sum += n;
-          for (int t = 0; t < n; ++t) {
-            const int w = sched_tile_index(x, slot, t, nwg / kXcds);
-            if (w < 0 || w >= total) return fail("tile index out of range", nwg, total, w);
-            if (seen[w]++) return fail("tile run twice", nwg, total, w);
+  for (int chunk : {1, 7, 11, 16, 22, 33, 64}) {
+    for (int nwg = 8; nwg <= 512; nwg += (chunk == kTileChunk ? 8 : 24)) {
+      for (int total = 0; total <= 3000; total += (total < 300 ? 1 : 37)) {
+        seen.assign(total, 0);
+        long long sum = 0;
+        for (int x = 0; x < kXcds; ++x) {
+          const int xt = sched_xcd_tiles(total, x, chunk);
+          for (int slot = 0; slot < nwg / kXcds; ++slot) {
+            const int n = sched_slot_tiles(xt, slot, nwg / kXcds);
+            sum += n;
+            for (int t = 0; t < n; ++t) {
+              const int w = sched_tile_index(x, slot, t, nwg / kXcds, chunk);
+              if (w < 0 || w >= total) return fail("tile index out of range", nwg, total, w);
+              if (seen[w]++) return fail("tile run twice", nwg, total, w);
+            }
           }
         }
+        if (sum != total) return fail("tiles lost", nwg, total, sum);
       }
-      if (sum != total) return fail("tiles lost", nwg, total, sum);
     }
   }
   // 2. the launcher's grid respects the row table at the real tile count
@@ -67,11 +69,12 @@ int main() {
         }
         const long long upper = ((long long)(M + BM - 1) / BM + G) * nt;
         if (total > upper) return fail("tile count above the launcher's bound", M, G, total);
-        const long long nwg = sched_workgroups(upper, cus, rt);
+        const int chunk = sched_chunk((int)(rng() % 5), nt);  // 0: the default size
+        const long long nwg = sched_workgroups(upper, cus, rt, chunk);
         if (nwg % kXcds || nwg < kXcds) return fail("grid not a multiple of 8", upper, cus, nwg);
-        if (sched_max_tiles((int)total, (int)nwg) > rt)
+        if (sched_max_tiles((int)total, (int)nwg, chunk) > rt)
           return fail("workgroup beyond the row table", total, nwg, rt);
-        if (sched_max_tiles((int)upper, (int)nwg) > rt)
+        if (sched_max_tiles((int)upper, (int)nwg, chunk) > rt)
           return fail("bound beyond the row table", upper, nwg, rt);
       }
     }
