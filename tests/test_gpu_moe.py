@@ -330,10 +330,14 @@ def tiled_layer(dsk, full_layer):
 
 @pytest.mark.parametrize("layout", ["row_major", "tiled"])
 @pytest.mark.parametrize("T,bias", [(64, False), (4096, False), (1, True), (4, True),
-                                    (16, True), (64, True), (100, True)])
+                                    (16, True), (64, True), (100, True), (2048, False),
+                                    (2048, True), (6000, False)])
 def test_fused_layer_matches_oracle(dsk, full_layer, tiled_layer, T, bias, layout):
     """Configs 0/1 (near-uniform routing) and 2 (Zipf-biased router), bf16, with
-    the expert weights row-major or fragment-tiled."""
+    the expert weights row-major or fragment-tiled. T = 2048, 4096 and 6000 deal
+    the large-group GEMMs' tiles one routed group (1, 2, 3 M tiles) per chunk;
+    with the Zipf router the groups are far from that size, so chunks straddle
+    groups."""
     from ds_kernels import synthetic as syn
     W, w1, w2, nsh, Wn = full_layer
     if layout == "tiled":
